@@ -1,0 +1,238 @@
+"""Benchmark of the DeepGenGraph attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--sections prefill,decode,...] [--no-cpu-baseline]
+
+Prints ONE JSON line. The headline `value` is config 2: bf16 causal prefill attention at Llama-2-7B shape
+(B=1, H=32, S=4096, D=128) in TFLOP/s under the reference's FLOP model 4*B*H*S^2*D/2 (run_kernel.py:24),
+one step = one attention forward over inputs already resident in HBM. The decode section reports config 5
+(split-KV decode over a 64 x 32 x 32768 x 128 fp16 cache) in GB/s of algorithmic K+V+q+o bytes; the other
+sections report configs 3 and 4, the config-2 block and the elementwise kernels. Kernel durations come from
+HIP events recorded on the stream the kernels are launched on (torch's current stream). The CPU baseline is
+the oracle (reference formula in PyTorch eager on the host cores) on a bounded sample of config 2.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+import torch
+
+METRIC = "attention TFLOP/s (% bf16 MFMA peak) + decode HBM GB/s, Llama-2-7B shapes"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16/fp16 MFMA
+PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
+
+
+def _events_time(fn, iters: int, warmup: int) -> list[float]:
+    """Runs fn warmup + iters times; returns per-call GPU durations (ms) from event pairs on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    for s, e in evs:
+        s.record()
+        fn()
+        e.record()
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in evs]
+
+
+def bench_prefill(args, dev):
+    from deepgengraph_amd import attention as A
+    from deepgengraph_amd import configs as C
+
+    cfg = C.CFG2
+    q, k, v, _ = C.attn_inputs(cfg, device=dev)
+    out = torch.empty_like(q)
+    fn = lambda: A.attention(q, k, v, causal=True, out=out)  # noqa: E731
+    for _ in range(args.warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        fn()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    per_launch = _events_time(fn, args.steps, 2)
+    kern_ms = statistics.mean(per_launch)
+    flops = cfg.reference_flops()
+    return dict(cfg=cfg, wall_ms=wall_ms, kern_ms=kern_ms, flops=flops, exact_flops=cfg.flops(),
+                tflops_wall=flops / (wall_ms * 1e-3) / 1e12, tflops_kern=flops / (kern_ms * 1e-3) / 1e12)
+
+
+def bench_decode(args, dev):
+    from deepgengraph_amd import attention as A
+    from deepgengraph_amd import configs as C
+
+    cfg = C.CFG5
+    q, kc, vc = C.decode_inputs(cfg, device=dev)
+    ws = torch.empty(A.decode_workspace_bytes(cfg.B, cfg.Hq, cfg.D, cfg.splits), dtype=torch.uint8, device=dev)
+    out = torch.empty_like(q)
+    fn = lambda: A.decode_attention(q, kc, vc, splits=cfg.splits, out=out, workspace=ws)  # noqa: E731
+    ms = statistics.mean(_events_time(fn, max(5, args.steps // 2), 2))
+    nbytes = cfg.bytes()
+    del kc, vc
+    torch.cuda.empty_cache()
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return dict(workload=cfg.name, ms=round(ms, 4), bytes=nbytes, gbps=round(gbps, 1),
+                frac=round(gbps / PEAK_HBM_GBPS, 4), splits=cfg.splits)
+
+
+def bench_prestep(args, dev):
+    from deepgengraph_amd import configs as C
+    from deepgengraph_amd import ops
+
+    cfg = C.CFG5
+    pre = C.decode_prestep_inputs(cfg, device=dev)
+    normed = torch.empty_like(pre["x"])
+    act = torch.empty(cfg.B, cfg.intermediate, dtype=cfg.dtype, device=dev)
+    e = pre["x"].element_size()
+    res = {}
+    ms = statistics.mean(_events_time(lambda: ops.rms_norm(normed, pre["x"], pre["w_norm"], C.LLAMA_EPS), 20, 3))
+    nb = e * (2 * pre["x"].numel() + pre["w_norm"].numel())
+    res["rms_norm_64x4096_f16"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1))
+    ms = statistics.mean(_events_time(lambda: ops.silu_and_mul(act, pre["gate_up"]), 20, 3))
+    nb = e * (pre["gate_up"].numel() + act.numel())
+    res["silu_and_mul_64x11008_f16"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1))
+    # config-2 sized elementwise kernels (bandwidth-meaningful sizes)
+    x = torch.randn(4096, 4096, device=dev).bfloat16()
+    w = torch.ones(4096, device=dev).bfloat16()
+    y = torch.empty_like(x)
+    ms = statistics.mean(_events_time(lambda: ops.rms_norm(y, x, w, 1e-6), 20, 3))
+    nb = 2 * (2 * x.numel() + w.numel())
+    res["rms_norm_4096x4096_bf16"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1),
+                                          frac=round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4))
+    qkv = torch.randn(4096, 3 * 4096, device=dev).bfloat16()
+    pos = torch.arange(4096, dtype=torch.int32, device=dev)
+    ms = statistics.mean(_events_time(
+        lambda: ops.rotary_embedding_online(pos, qkv[:, :4096], qkv[:, 4096:8192], 128, 1e4), 20, 3))
+    nb = 2 * 2 * (2 * 4096 * 4096) + 4 * 4096
+    res["rotary_4096tok_32+32heads_bf16"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1),
+                                                 frac=round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4))
+    gu = torch.randn(4096, 2 * 11008, device=dev).bfloat16()
+    a = torch.empty(4096, 11008, device=dev, dtype=torch.bfloat16)
+    ms = statistics.mean(_events_time(lambda: ops.silu_and_mul(a, gu), 20, 3))
+    nb = 2 * (gu.numel() + a.numel())
+    res["silu_and_mul_4096x11008_bf16"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1),
+                                               frac=round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4))
+    return res
+
+
+def bench_variants(args, dev):
+    from deepgengraph_amd import attention as A
+    from deepgengraph_amd import configs as C
+
+    res = {}
+    cfg = C.CFG3
+    q, k, v, _ = C.attn_inputs(cfg, device=dev)
+    ms = statistics.mean(_events_time(
+        lambda: A.attention(q, k, v, causal=True, softcap=cfg.softcap, window=cfg.window), 5, 1))
+    res["cfg3_gemma2"] = dict(ms=round(ms, 4), tflops=round(cfg.flops() / (ms * 1e-3) / 1e12, 1),
+                              frac=round(cfg.flops() / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))
+    del q, k, v
+    cfg = C.CFG4
+    q, k, v, _ = C.attn_inputs(cfg, device=dev)
+    ms = statistics.mean(_events_time(lambda: A.topk_indices(A.h2o_attention(q, k, v)[1], cfg.topk), 5, 1))
+    res["cfg4_h2o_fwd_colsum_topk"] = dict(ms=round(ms, 4),
+                                           tflops=round(cfg.reference_flops() / (ms * 1e-3) / 1e12, 1),
+                                           frac=round(cfg.reference_flops() / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))
+    return res
+
+
+def bench_block(args, dev):
+    from deepgengraph_amd import configs as C
+    from deepgengraph_amd.llama import LlamaAttentionBlock
+
+    inp = C.llama_block_inputs(device=dev)
+    blk = LlamaAttentionBlock(inp["w_norm"], inp["w_qkv"], inp["w_o"], heads=32, kv_heads=32, eps=C.LLAMA_EPS,
+                              rope_theta=C.LLAMA_THETA)
+    ms = statistics.mean(_events_time(lambda: blk(inp["x"]), 10, 2))
+    return dict(ms=round(ms, 4))
+
+
+def cpu_baseline(target_s: float = 10.0):
+    """Oracle (reference formula, PyTorch eager on the host CPU) on a bounded sample of config 2: 8 of the 32
+    heads over the full sequence. Repeated until ~target_s of CPU time; the median run is reported."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from deepgengraph_amd import configs as C
+    from oracle import attention as oa
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    heads = 8
+    q, k, v, _ = C.attn_inputs(C.CFG2)
+    q, k, v = (t[:, :, :heads].contiguous() for t in (q, k, v))
+    oa.attention(q[:, :256], k[:, :256], v[:, :256])  # warm-up
+    times, t_start = [], time.perf_counter()
+    while (time.perf_counter() - t_start < target_s and len(times) < 5) or len(times) < 1:
+        t0 = time.perf_counter()
+        oa.attention(q, k, v, causal=True)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    flops = 4.0 * 1 * heads * 4096 * 4096 * 128 / 2
+    return {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"config 2 attention, {heads} of 32 heads, full S=4096, bf16, median of "
+                                      f"{len(times)} runs ({t:.2f} s each), same FLOP model",
+            "cpu": platform.processor() or platform.machine()}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--sections", default="prefill,decode,prestep,variants,block")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py: this build measures one GPU only (the attention hot path runs on a single GPU; multi-GPU "
+              f"sharding is not built); --gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    sections = set(args.sections.split(","))
+    extra = {}
+    pre = bench_prefill(args, dev)
+    cfg = pre["cfg"]
+    if "decode" in sections:
+        extra["decode"] = bench_decode(args, dev)
+    if "prestep" in sections:
+        extra["elementwise"] = bench_prestep(args, dev)
+    if "variants" in sections:
+        extra["variants"] = bench_variants(args, dev)
+    if "block" in sections:
+        extra["cfg2_block_ms"] = bench_block(args, dev)["ms"]
+    line = {
+        "metric": METRIC,
+        "value": round(pre["tflops_wall"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(pre["wall_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "cfg2_llama2_7b_prefill_attention", "B": cfg.B, "S": cfg.Sq, "H": cfg.Hq,
+                   "D": cfg.D, "causal": True, "flop_model": "4*B*H*S^2*D/2 (run_kernel.py:24)",
+                   "flops_per_step": pre["flops"], "exact_pair_flops": pre["exact_flops"]},
+        "roofline": {"bound": "mfma", "achieved": round(pre["tflops_kern"], 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(pre["tflops_kern"] / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel_ms": round(pre["kern_ms"], 5)},
+    }
+    line.update(extra)
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,146 @@
+"""Attention entry points on MI355X: prefill (causal / soft-cap / sliding window / GQA), H2O column sums,
+top-k key selection, and split-KV decode. Each allocates its outputs with torch on the inputs' device (as the
+callables produced by the reference's compile() do, to_triton.cpp:579-590) and launches the HIP kernels of
+libdgg_hip.so on the current stream.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+
+def _check_bshd(name: str, t: torch.Tensor):
+    if t.dim() != 4:
+        raise RuntimeError(f"{name}: expected [B, S, H, D], got shape {tuple(t.shape)}")
+    if t.stride(-1) != 1:
+        raise RuntimeError(f"{name}: head dimension must be contiguous (stride {t.stride(-1)})")
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool = True, softcap: float = 0.0,
+              window: int = 0, scale: float | None = None, return_lse: bool = False, ref_rounding: bool = False,
+              out: torch.Tensor | None = None):
+    """Fused attention forward. q [B, Sq, Hq, D]; k, v [B, Sk, Hkv, D]; returns out [B, Sq, Hq, D] (q.dtype)
+    and, with return_lse, lse [B, Hq, Sq] fp32 (natural log).
+
+    Semantics of Attn.forward / Gemma2.forward (deepgengraph_exp/cases/kernels/attn.py:18-34,
+    gemma2.py:19-38): scores = q.k^T * scale (default 1/sqrt(D)), optional softcap*tanh(scores/softcap),
+    bottom-right aligned causal mask (attn.py:22-23), optional sliding window (key j visible iff
+    i + Sk - Sq - j < window), fp32 softmax, P.V. ref_rounding rounds the scores to the input dtype at the
+    reference's rounding points (slower; used for H2O selection parity)."""
+    dev = _lib.require_gpu(q, k, v, out)
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _check_bshd(name, t)
+    B, Sq, Hq, D = q.shape
+    Sk, Hkv = k.shape[1], k.shape[2]
+    if k.shape[0] != B or v.shape != k.shape or k.shape[3] != D:
+        raise RuntimeError(f"attention: incompatible shapes q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise RuntimeError("attention: q, k, v dtypes differ")
+    if out is None:
+        out = torch.empty(B, Sq, Hq, D, dtype=q.dtype, device=q.device)
+    else:
+        _check_bshd("out", out)
+        if out.shape != q.shape or out.dtype != q.dtype:
+            raise RuntimeError("attention: out must match q in shape and dtype")
+    lse = torch.empty(B, Hq, Sq, dtype=torch.float32, device=q.device) if return_lse else None
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    flags = (_lib.ATTN_CAUSAL if causal else 0) | (_lib.ATTN_REF_ROUNDING if ref_rounding else 0)
+    strides = _lib.int64_array([*q.stride()[:3], *k.stride()[:3], *v.stride()[:3], *out.stride()[:3]])
+    _lib.call("dgg_attn_prefill", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out), _lib.ptr(lse), B, Sq, Sk,
+              Hq, Hkv, D, strides, scale, float(softcap or 0.0), int(window or 0), flags, _lib.dtype_code(q.dtype),
+              _lib.stream_handle(dev))
+    return (out, lse) if return_lse else out
+
+
+def attention_colsum(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor, *, causal: bool = True,
+                     softcap: float = 0.0, window: int = 0, scale: float | None = None,
+                     ref_rounding: bool = False) -> torch.Tensor:
+    """Column sums of the softmax probabilities over the query axis, per query head: [B, Hq, Sk] fp32, recomputed
+    from q, k and the lse written by attention(..., return_lse=True) with the same options."""
+    dev = _lib.require_gpu(q, k, lse)
+    _check_bshd("q", q)
+    _check_bshd("k", k)
+    B, Sq, Hq, D = q.shape
+    Sk, Hkv = k.shape[1], k.shape[2]
+    if lse.shape != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise RuntimeError(f"attention_colsum: lse must be contiguous fp32 [{B}, {Hq}, {Sq}]")
+    colsum = torch.empty(B, Hq, Sk, dtype=torch.float32, device=q.device)
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    flags = (_lib.ATTN_CAUSAL if causal else 0) | (_lib.ATTN_REF_ROUNDING if ref_rounding else 0)
+    strides = _lib.int64_array([*q.stride()[:3], *k.stride()[:3]])
+    _lib.call("dgg_attn_colsum", _lib.ptr(q), _lib.ptr(k), _lib.ptr(lse), _lib.ptr(colsum), B, Sq, Sk, Hq, Hkv, D,
+              strides, scale, float(softcap or 0.0), int(window or 0), flags, _lib.dtype_code(q.dtype),
+              _lib.stream_handle(dev))
+    return colsum
+
+
+def h2o_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, ref_rounding: bool = True):
+    """H2O.forward (deepgengraph_exp/cases/kernels/h2o.py:18-38): causal attention output [B, S, H, D] and the fp32
+    probability column sums h2o_score [B, Hkv, Sk]. Two launches: the forward kernel (which also writes the row
+    lse) and the column-sum kernel. With GQA the per-query-head sums are averaged over each KV group (the
+    convention of roco.py:40-41)."""
+    out, lse = attention(q, k, v, causal=True, return_lse=True, ref_rounding=ref_rounding)
+    colsum = attention_colsum(q, k, lse, causal=True, ref_rounding=ref_rounding)
+    Hq, Hkv = q.shape[2], k.shape[2]
+    if Hq != Hkv:
+        colsum = colsum.view(q.shape[0], Hkv, Hq // Hkv, -1).mean(dim=2)
+    return out, colsum
+
+
+def topk_indices(scores: torch.Tensor, k: int) -> torch.Tensor:
+    """deepgengraph_exp/cases/models/h2o.py:51-52 (torch.topk then sort of the indices) with a defined tie
+    order: the k largest of each row of scores [..., n] (fp32), ties broken by the lowest index, returned as int64
+    indices [..., k] in ascending order."""
+    dev = _lib.require_gpu(scores)
+    if scores.dtype != torch.float32 or not scores.is_contiguous():
+        raise RuntimeError("topk_indices: scores must be a contiguous fp32 tensor")
+    n = scores.shape[-1]
+    rows = scores.numel() // n if n else 0
+    out = torch.empty(*scores.shape[:-1], k, dtype=torch.int64, device=scores.device)
+    _lib.call("dgg_topk_indices", _lib.ptr(scores), rows, n, int(k), _lib.ptr(out), _lib.stream_handle(dev))
+    return out
+
+
+def decode_workspace_bytes(B: int, Hq: int, D: int, splits: int) -> int:
+    return int(_lib.load().dgg_attn_decode_workspace_bytes(B, Hq, D, splits))
+
+
+def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *, splits: int = 64,
+                     scale: float | None = None, return_lse: bool = False, out: torch.Tensor | None = None,
+                     workspace: torch.Tensor | None = None):
+    """Attn.forward with q_len == 1 (attn.py:22-23: nothing masked) over a [B, Hkv, L, D] KV cache, computed as a
+    split-KV pass (`splits` slices of the cache) followed by a log-sum-exp merge. q [B, Hq, D] -> out
+    [B, Hq, D] (+ lse [B, Hq] fp32). `workspace` (uint8/any, >= decode_workspace_bytes bytes) may be passed to
+    avoid an allocation per call."""
+    dev = _lib.require_gpu(q, k_cache, v_cache, out, workspace)
+    if q.dim() != 3 or k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise RuntimeError("decode_attention: expected q [B, Hq, D] and k/v caches [B, Hkv, L, D]")
+    B, Hq, D = q.shape
+    Hkv, L = k_cache.shape[1], k_cache.shape[2]
+    if k_cache.shape[0] != B or k_cache.shape[3] != D:
+        raise RuntimeError("decode_attention: cache shape does not match q")
+    for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
+        if t.stride(-1) != 1:
+            raise RuntimeError(f"decode_attention: {name} head dimension must be contiguous")
+    if not (q.dtype == k_cache.dtype == v_cache.dtype):
+        raise RuntimeError("decode_attention: dtypes differ")
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=q.dtype, device=q.device)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise RuntimeError("decode_attention: out must match q")
+    need = decode_workspace_bytes(B, Hq, D, splits)
+    if need < 0:
+        raise RuntimeError("decode_attention: invalid sizes")
+    if workspace is None:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
+    ws_bytes = workspace.numel() * workspace.element_size()
+    lse = torch.empty(B, Hq, dtype=torch.float32, device=q.device) if return_lse else None
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    strides = _lib.int64_array([*q.stride()[:2], *k_cache.stride()[:3], *v_cache.stride()[:3], *out.stride()[:2]])
+    _lib.call("dgg_attn_decode", _lib.ptr(q), _lib.ptr(k_cache), _lib.ptr(v_cache), _lib.ptr(out), _lib.ptr(lse),
+              _lib.ptr(workspace), ws_bytes, B, Hq, Hkv, L, D, strides, int(splits), scale,
+              _lib.dtype_code(q.dtype), _lib.stream_handle(dev))
+    return (out, lse) if return_lse else out

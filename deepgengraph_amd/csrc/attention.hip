@@ -1,0 +1,613 @@
+// Fused online-softmax attention for gfx950 (CDNA4): prefill forward (causal / sliding window / tanh
+// soft-cap / GQA) and the H2O probability column-sum pass.
+//
+// Tiling (forward). A workgroup of 4 wave64s owns BM = 128 query rows of one (batch, head); wave w owns
+// rows 32w..32w+31. K/V are streamed in tiles of BN keys through double-buffered LDS: K row-major
+// [key][d] and V transposed [d][key]. Both products run on v_mfma_f32_32x32x16_{bf16,f16}:
+//   S^T (BN x 32)  = K (BN x D) . Q^T (D x 32)     A = K from LDS, B = Q held in VGPRs for the whole loop
+//   O^T (D x 32)  += V^T (D x BN) . P^T (BN x 32)  A = V^T from LDS, B = P straight from the S^T accumulator
+// Computing S transposed puts one query per lane (column n = lane % 32) with its keys spread over the
+// lane's accumulator registers and the partner lane (lane ^ 32). Row max / row sum are therefore in-lane
+// plus one cross-half exchange, and the fp32 accumulator, rounded to 16 bits, is already laid out as the
+// B operand of the P.V product (both operands use the same key order, so no LDS round trip for P).
+// Softmax runs in the exp2 domain with a lazily-updated row maximum: O and l are rescaled only when a
+// row's maximum grows by more than 2^8, so P stays <= 256 and the 64-register O rescale is rare.
+// Causal / window tiles are skipped per workgroup; only tiles that straddle the mask boundary (or the
+// ragged end of K) evaluate the per-element mask. Workgroups are ordered longest-first and grouped by
+// head inside each XCD (blockIdx round-robins over the 8 XCDs) so the K/V of a head stay in one L2.
+#include <algorithm>
+
+#include "common.h"
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kBM = 32 * kWaves;  // query rows per forward workgroup
+constexpr float kRescaleThreshold = 8.0f;  // log2 units
+
+struct AttnParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;
+  float* colsum;
+  int64_t q_sb, q_ss, q_sh;
+  int64_t k_sb, k_ss, k_sh;
+  int64_t v_sb, v_ss, v_sh;
+  int64_t o_sb, o_ss, o_sh;
+  int B, Sq, Sk, Hq, Hkv, group;
+  int n_tiles;   // forward: query tiles; colsum: key tiles
+  int causal;
+  int window;    // 0 = none
+  int offset;    // Sk - Sq (bottom-right aligned causal mask)
+  float scale;
+  float ref_div;  // 1 / scale rounded to fp32 (== fp32 sqrt(D) for the usual scale): the reference divides
+  float c_fast;  // scale * log2(e): converts raw scores to the exp2 domain
+  float inv_softcap;
+  float softcap;
+  float sc_a;    // 2 * scale / softcap * log2(e)
+  float sc_b;    // softcap * log2(e)
+};
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ float round_t(float x) {
+  return to_f<typename T::scalar>(to_s<typename T::scalar>(x));
+}
+
+// Score transform shared by the forward and column-sum kernels. Returns the value whose exp2 (after the
+// row maximum / lse is subtracted and `c` applied) is the unnormalised probability:
+//   fast path (no soft-cap, no reference rounding): the raw fp32 score; the caller multiplies by c_fast.
+//   otherwise: the score already in the exp2 domain (c = 1).
+template <typename T, bool SOFTCAP, bool REFROUND>
+__device__ __forceinline__ float score_value(float s, const AttnParams& p) {
+  if constexpr (REFROUND) {
+    // deepgengraph_exp/cases/kernels/attn.py:29 / gemma2.py:29-33: each step rounded to the input dtype;
+    // `/ math.sqrt(D)` is an fp32 true division before the rounding.
+    s = round_t<T>(s);
+    s = round_t<T>(s / p.ref_div);
+    if constexpr (SOFTCAP) {
+      s = round_t<T>(s / p.softcap);
+      s = round_t<T>(tanhf(s));
+      s = round_t<T>(s * p.softcap);
+    }
+    return s * kLog2e;
+  } else if constexpr (SOFTCAP) {
+    // softcap * tanh(s * scale / softcap) in the exp2 domain, tanh(y) = 1 - 2 / (exp(2y) + 1).
+    const float e = fast_exp2(s * p.sc_a);
+    return fmaf(fast_rcp(e + 1.0f), -2.0f * p.sc_b, p.sc_b);
+  } else {
+    return s;
+  }
+}
+
+template <bool SOFTCAP, bool REFROUND>
+__device__ __forceinline__ float score_coeff(const AttnParams& p) {
+  return (SOFTCAP || REFROUND) ? 1.0f : p.c_fast;
+}
+
+// Maps blockIdx.x to (tile, batch*head). Longest tiles first; when the (batch, head) count divides by 8,
+// each XCD gets a contiguous group of heads so their K/V are shared through that XCD's L2.
+__device__ __forceinline__ void map_block(int n_tiles, int bh_count, bool reverse, int& tile, int& bh) {
+  const int bid = blockIdx.x;
+  int t_major, bh_minor;
+  if ((bh_count & 7) == 0) {
+    const int hpx = bh_count >> 3;
+    const int xcd = bid & 7, local = bid >> 3;
+    t_major = local / hpx;
+    bh_minor = xcd * hpx + (local - t_major * hpx);
+  } else {
+    t_major = bid / bh_count;
+    bh_minor = bid - t_major * bh_count;
+  }
+  tile = reverse ? n_tiles - 1 - t_major : t_major;
+  bh = bh_minor;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Forward kernel.
+// ------------------------------------------------------------------------------------------------
+template <typename T, int D, int BN, bool MASK, bool SOFTCAP, bool REFROUND>
+__global__ void __launch_bounds__(kThreads) attn_fwd_kernel(AttnParams p) {
+  typedef typename T::scalar S;
+  typedef typename T::vec8 V8;
+  typedef typename T::vec4 V4;
+  constexpr int KP = D + 8;   // padded K row (elements)
+  constexpr int VP = BN + 4;  // padded V^T row (elements)
+  constexpr int NKK = D / 16;      // MFMA k-steps over the head dim
+  constexpr int NMB = BN / 32;     // 32-key blocks per tile
+  constexpr int NDB = D / 32;      // 32-wide head-dim blocks of O^T
+  constexpr int NPK = BN / 16;     // MFMA k-steps over keys in P.V
+  constexpr int CHUNKS = BN * D / 8;
+  constexpr int CPT = CHUNKS / kThreads;  // 16-byte chunks per thread per tile (K and V each)
+  static_assert(CHUNKS % kThreads == 0, "tile must split evenly over the workgroup");
+
+  __shared__ __attribute__((aligned(16))) S Ks[2][BN][KP];
+  __shared__ __attribute__((aligned(16))) S Vt[2][D][VP];
+
+  int qt, bh;
+  map_block(p.n_tiles, p.B * p.Hq, true, qt, bh);
+  const int b = bh / p.Hq, h = bh - b * p.Hq;
+  const int hk = h / p.group;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, r = lane & 31, g = lane >> 5;
+  const int q0 = qt * kBM;
+  const int qi = q0 + 32 * w + r;  // this lane's query row
+
+  const S* qp = static_cast<const S*>(p.q) + b * p.q_sb + h * p.q_sh;
+  const S* kp = static_cast<const S*>(p.k) + b * p.k_sb + hk * p.k_sh;
+  const S* vp = static_cast<const S*>(p.v) + b * p.v_sb + hk * p.v_sh;
+
+  // Q fragment (B operand of S^T = K.Q^T): lane holds query qi, head-dim elements 16kk + 8g .. +8.
+  V8 qf[NKK];
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk) {
+    if (qi < p.Sq) qf[kk] = ld16<V8>(qp + (int64_t)qi * p.q_ss + 16 * kk + 8 * g);
+    else qf[kk] = V8{};
+  }
+
+  // Key range of this query tile.
+  const int q_last = min(q0 + kBM, p.Sq) - 1;
+  int k_begin = 0, k_end = p.Sk;
+  if (p.causal) k_end = min(p.Sk, q_last + p.offset + 1);
+  if (p.window > 0) k_begin = max(0, q0 + p.offset - p.window + 1);
+  const int t_begin = k_begin / BN;
+  const int t_end = k_end > k_begin ? (k_end + BN - 1) / BN : t_begin;
+
+  f32x16 oacc[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i) oacc[i] = f32x16{};
+  float m_run = -INFINITY;  // reference maximum (value units)
+  float l_run = 0.f;        // partial row sum (this lane's half of the keys)
+  const float c = score_coeff<SOFTCAP, REFROUND>(p);
+
+  V8 kreg[CPT], vreg[CPT];
+  auto load_tile = [&](int t) {
+    const int kb = t * BN;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int ch = tid + i * kThreads;
+      {  // K: lanes run along the head dim (coalesced rows)
+        const int key = ch / (D / 8), dc = ch % (D / 8);
+        const int kg = kb + key;
+        kreg[i] = kg < p.Sk ? ld16<V8>(kp + (int64_t)kg * p.k_ss + dc * 8) : V8{};
+      }
+      {  // V: lanes run along keys so the transposed LDS writes are conflict-free
+        const int key = ch % BN, dc = ch / BN;
+        const int kg = kb + key;
+        vreg[i] = kg < p.Sk ? ld16<V8>(vp + (int64_t)kg * p.v_ss + dc * 8) : V8{};
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int ch = tid + i * kThreads;
+      {
+        const int key = ch / (D / 8), dc = ch % (D / 8);
+        *reinterpret_cast<V8*>(&Ks[buf][key][dc * 8]) = kreg[i];
+      }
+      {
+        const int key = ch % BN, dc = ch / BN;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) Vt[buf][dc * 8 + e][key] = vreg[i][e];
+      }
+    }
+  };
+
+  if (t_begin < t_end) {
+    load_tile(t_begin);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int t = t_begin; t < t_end; ++t) {
+    const int buf = (t - t_begin) & 1;
+    const bool has_next = t + 1 < t_end;
+    if (has_next) load_tile(t + 1);
+
+    // S^T = K . Q^T
+    f32x16 sacc[NMB];
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) sacc[mb] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb) {
+        const V8 a = *reinterpret_cast<const V8*>(&Ks[buf][mb * 32 + r][16 * kk + 8 * g]);
+        sacc[mb] = mfma32(a, qf[kk], sacc[mb]);
+      }
+    }
+
+    // Scores -> values, mask, row max.
+    const int kb = t * BN;
+    bool need_mask = kb + BN > p.Sk;
+    if constexpr (MASK) {
+      if (p.causal && kb + BN - 1 > q0 + p.offset) need_mask = true;
+      if (p.window > 0 && kb < q_last + p.offset - p.window + 1) need_mask = true;
+    }
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float x = score_value<T, SOFTCAP, REFROUND>(sacc[mb][j], p);
+        if (need_mask) {
+          const int kj = kb + mb * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
+          bool ok = kj < p.Sk;
+          if constexpr (MASK) {
+            const int rel = qi + p.offset - kj;  // query position minus key position
+            if (p.causal) ok = ok && rel >= 0;
+            if (p.window > 0) ok = ok && rel < p.window;
+          }
+          x = ok ? x : -INFINITY;
+        }
+        sacc[mb][j] = x;
+        mloc = fmaxf(mloc, x);
+      }
+    }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float m_new = fmaxf(m_run, mloc);
+    const bool need = m_new * c > m_run * c + kRescaleThreshold;
+    if (__any(need)) {
+      const float alpha = need ? fast_exp2((m_run - m_new) * c) : 1.0f;
+      if (need) m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < NDB; ++i) oacc[i] *= alpha;
+    }
+    const float mc = m_run == -INFINITY ? 0.f : m_run * c;
+
+    // P = exp2(v*c - m*c), row-sum, pack to 16-bit B operands, O^T += V^T . P^T
+#pragma unroll
+    for (int kk = 0; kk < NPK; ++kk) {
+      f32x8 pv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float pe = fast_exp2(fmaf(sacc[kk >> 1][8 * (kk & 1) + e], c, -mc));
+        l_run += pe;
+        pv[e] = pe;
+      }
+      const V8 pb = from_f32x8<V8>(pv);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const V4 lo = *reinterpret_cast<const V4*>(&Vt[buf][db * 32 + r][16 * kk + 4 * g]);
+        const V4 hi = *reinterpret_cast<const V4*>(&Vt[buf][db * 32 + r][16 * kk + 8 + 4 * g]);
+        const V8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        oacc[db] = mfma32(a, pb, oacc[db]);
+      }
+    }
+
+    if (has_next) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: full row sum, normalise, store O (4 consecutive head-dim elements per store) and lse.
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = 1.0f / l_tot;
+  if (qi < p.Sq) {
+    S* op = static_cast<S*>(p.o) + b * p.o_sb + (int64_t)qi * p.o_ss + h * p.o_sh;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        V4 ov;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ov[e] = to_s<S>(oacc[db][4 * jj + e] * inv);
+        *reinterpret_cast<V4*>(op + db * 32 + 8 * jj + 4 * g) = ov;
+      }
+    }
+    if (p.lse != nullptr && g == 0) {
+      const float lse2 = m_run == -INFINITY ? -INFINITY : m_run * c + fast_log2(l_tot);
+      p.lse[(int64_t)bh * p.Sq + qi] = lse2 * kLn2;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Column-sum kernel: colsum[b,h,j] = sum_i exp(score_ij - lse_i). A workgroup owns 128 keys (32 per wave,
+// held in VGPRs as the B operand); query tiles of 64 rows stream through double-buffered LDS together
+// with their lse. S (64 x 32) = Q . K^T puts one key per lane, so each lane sums its own column.
+// ------------------------------------------------------------------------------------------------
+constexpr int kCBQ = 64;   // query rows per tile
+constexpr int kCBK = 32 * kWaves;  // keys per workgroup
+
+template <typename T, int D, bool MASK, bool SOFTCAP, bool REFROUND>
+__global__ void __launch_bounds__(kThreads) attn_colsum_kernel(AttnParams p) {
+  typedef typename T::scalar S;
+  typedef typename T::vec8 V8;
+  constexpr int QP = D + 8;
+  constexpr int NKK = D / 16;
+  constexpr int NMB = kCBQ / 32;
+  constexpr int CHUNKS = kCBQ * D / 8;
+  constexpr int CPT = (CHUNKS + kThreads - 1) / kThreads;
+
+  __shared__ __attribute__((aligned(16))) S Qs[2][kCBQ][QP];
+  __shared__ float Ls[2][kCBQ];
+
+  int kt, bh;
+  map_block(p.n_tiles, p.B * p.Hq, false, kt, bh);
+  const int b = bh / p.Hq, h = bh - b * p.Hq;
+  const int hk = h / p.group;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, r = lane & 31, g = lane >> 5;
+  const int k0 = kt * kCBK;
+  const int kj = k0 + 32 * w + r;  // this lane's key
+
+  const S* qp = static_cast<const S*>(p.q) + b * p.q_sb + h * p.q_sh;
+  const S* kp = static_cast<const S*>(p.k) + b * p.k_sb + hk * p.k_sh;
+  const float* lsep = p.lse + (int64_t)bh * p.Sq;
+
+  V8 kf[NKK];
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk) {
+    if (kj < p.Sk) kf[kk] = ld16<V8>(kp + (int64_t)kj * p.k_ss + 16 * kk + 8 * g);
+    else kf[kk] = V8{};
+  }
+
+  // Query range that can see any key of this tile.
+  const int k_last = min(k0 + kCBK, p.Sk) - 1;
+  int q_begin = 0, q_end = p.Sq;
+  if (p.causal) q_begin = max(0, k0 - p.offset);
+  if (p.window > 0) q_end = min(p.Sq, k_last - p.offset + p.window);
+  const int t_begin = q_begin / kCBQ;
+  const int t_end = q_end > q_begin ? (q_end + kCBQ - 1) / kCBQ : t_begin;
+  const float c = score_coeff<SOFTCAP, REFROUND>(p);
+
+  V8 qreg[CPT];
+  float lreg = 0.f;
+  auto load_tile = [&](int t) {
+    const int qb = t * kCBQ;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int ch = tid + i * kThreads;
+      if (CHUNKS % kThreads == 0 || ch < CHUNKS) {
+        const int row = ch / (D / 8), dc = ch % (D / 8);
+        const int qg = qb + row;
+        qreg[i] = qg < p.Sq ? ld16<V8>(qp + (int64_t)qg * p.q_ss + dc * 8) : V8{};
+      }
+    }
+    if (tid < kCBQ) {
+      const int qg = qb + tid;
+      // Rows past the end get +inf so that their probability is exp2(-inf) = 0.
+      lreg = qg < p.Sq ? lsep[qg] * kLog2e : INFINITY;
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int ch = tid + i * kThreads;
+      if (CHUNKS % kThreads == 0 || ch < CHUNKS) {
+        const int row = ch / (D / 8), dc = ch % (D / 8);
+        *reinterpret_cast<V8*>(&Qs[buf][row][dc * 8]) = qreg[i];
+      }
+    }
+    if (tid < kCBQ) Ls[buf][tid] = lreg;
+  };
+
+  if (t_begin < t_end) {
+    load_tile(t_begin);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  float col = 0.f;
+  for (int t = t_begin; t < t_end; ++t) {
+    const int buf = (t - t_begin) & 1;
+    const bool has_next = t + 1 < t_end;
+    if (has_next) load_tile(t + 1);
+
+    f32x16 sacc[NMB];
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) sacc[mb] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb) {
+        const V8 a = *reinterpret_cast<const V8*>(&Qs[buf][mb * 32 + r][16 * kk + 8 * g]);
+        sacc[mb] = mfma32(a, kf[kk], sacc[mb]);
+      }
+    }
+
+    const int qb = t * kCBQ;
+    bool need_mask = qb + kCBQ > p.Sq || k0 + kCBK > p.Sk;
+    if constexpr (MASK) {
+      if (p.causal && qb + p.offset < k_last) need_mask = true;
+      if (p.window > 0 && qb + kCBQ - 1 + p.offset - k0 >= p.window) need_mask = true;
+    }
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int row = mb * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
+        const float x = score_value<T, SOFTCAP, REFROUND>(sacc[mb][j], p);
+        float pe = fast_exp2(fmaf(x, c, -Ls[buf][row]));
+        if (need_mask) {
+          const int qg = qb + row;
+          bool ok = qg < p.Sq && kj < p.Sk;
+          if constexpr (MASK) {
+            const int rel = qg + p.offset - kj;
+            if (p.causal) ok = ok && rel >= 0;
+            if (p.window > 0) ok = ok && rel < p.window;
+          }
+          pe = ok ? pe : 0.f;
+        }
+        col += pe;
+      }
+    }
+
+    if (has_next) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+  col += __shfl_xor(col, 32, 64);
+  if (g == 0 && kj < p.Sk) p.colsum[(int64_t)bh * p.Sk + kj] = col;
+}
+
+template <typename T, int D, int BN, bool MASK, bool SOFTCAP, bool REFROUND>
+void launch_fwd(const AttnParams& p, hipStream_t st) {
+  const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
+  hipLaunchKernelGGL((attn_fwd_kernel<T, D, BN, MASK, SOFTCAP, REFROUND>), dim3(grid), dim3(kThreads), 0, st, p);
+}
+
+template <typename T, int D, bool MASK, bool SOFTCAP, bool REFROUND>
+void launch_colsum(const AttnParams& p, hipStream_t st) {
+  const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
+  hipLaunchKernelGGL((attn_colsum_kernel<T, D, MASK, SOFTCAP, REFROUND>), dim3(grid), dim3(kThreads), 0, st, p);
+}
+
+template <typename T, int D, bool MASK, bool SOFTCAP>
+void pick_fwd_ref(const AttnParams& p, bool ref, hipStream_t st) {
+  constexpr int BN = D >= 256 ? 32 : 64;
+  if (ref) launch_fwd<T, D, BN, MASK, SOFTCAP, true>(p, st);
+  else launch_fwd<T, D, BN, MASK, SOFTCAP, false>(p, st);
+}
+template <typename T, int D>
+void pick_fwd(const AttnParams& p, bool ref, hipStream_t st) {
+  const bool mask = p.causal || p.window > 0;
+  const bool sc = p.softcap > 0.f;
+  if (mask) {
+    if (sc) pick_fwd_ref<T, D, true, true>(p, ref, st);
+    else pick_fwd_ref<T, D, true, false>(p, ref, st);
+  } else {
+    if (sc) pick_fwd_ref<T, D, false, true>(p, ref, st);
+    else pick_fwd_ref<T, D, false, false>(p, ref, st);
+  }
+}
+template <typename T, int D, bool MASK, bool SOFTCAP>
+void pick_col_ref(const AttnParams& p, bool ref, hipStream_t st) {
+  if (ref) launch_colsum<T, D, MASK, SOFTCAP, true>(p, st);
+  else launch_colsum<T, D, MASK, SOFTCAP, false>(p, st);
+}
+template <typename T, int D>
+void pick_col(const AttnParams& p, bool ref, hipStream_t st) {
+  const bool mask = p.causal || p.window > 0;
+  const bool sc = p.softcap > 0.f;
+  if (mask) {
+    if (sc) pick_col_ref<T, D, true, true>(p, ref, st);
+    else pick_col_ref<T, D, true, false>(p, ref, st);
+  } else {
+    if (sc) pick_col_ref<T, D, false, true>(p, ref, st);
+    else pick_col_ref<T, D, false, false>(p, ref, st);
+  }
+}
+
+// Shared host-side validation of the attention arguments.
+int validate_attn(const char* op, const void* q, const void* k, int64_t B, int64_t Sq, int64_t Sk, int64_t Hq,
+                  int64_t Hkv, int64_t D, const int64_t* strides, int nstrides, float scale, float softcap,
+                  int64_t window, int dtype) {
+  DGG_REQUIRE(dtype == DGG_F16 || dtype == DGG_BF16, DGG_ERR_DTYPE,
+              "%s: dtype code %d not supported (attention kernels take f16 or bf16)", op, dtype);
+  DGG_REQUIRE(D == 64 || D == 128 || D == 256, DGG_ERR_UNSUPPORTED, "%s: head_dim %lld not supported (64, 128, 256)",
+              op, (long long)D);
+  DGG_REQUIRE(B >= 0 && Sq >= 0 && Sk >= 0, DGG_ERR_SHAPE, "%s: negative size", op);
+  DGG_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0, DGG_ERR_SHAPE,
+              "%s: query heads (%lld) must be a positive multiple of kv heads (%lld)", op, (long long)Hq,
+              (long long)Hkv);
+  DGG_REQUIRE(Sq < (1ll << 30) && Sk < (1ll << 30) && B < (1ll << 20) && Hq < (1ll << 16), DGG_ERR_SHAPE,
+              "%s: size too large", op);
+  DGG_REQUIRE(B * Hq * ((std::max(Sq, Sk) + 127) / 128) < (1ll << 31), DGG_ERR_SHAPE, "%s: grid too large", op);
+  DGG_REQUIRE(strides != nullptr, DGG_ERR_NULL, "%s: strides is NULL", op);
+  for (int i = 0; i < nstrides; ++i)
+    DGG_REQUIRE(strides[i] >= 0 && strides[i] % 8 == 0, DGG_ERR_STRIDE,
+                "%s: stride[%d] = %lld must be a non-negative multiple of 8 elements", op, i, (long long)strides[i]);
+  DGG_REQUIRE(std::isfinite(scale) && scale > 0.f, DGG_ERR_SHAPE, "%s: scale must be finite and > 0", op);
+  DGG_REQUIRE(softcap >= 0.f && std::isfinite(softcap), DGG_ERR_SHAPE, "%s: softcap must be >= 0 (0 = off)", op);
+  DGG_REQUIRE(window >= 0 && window < (1ll << 30), DGG_ERR_SHAPE, "%s: window must be >= 0 (0 = off)", op);
+  if (B == 0 || Sq == 0 || Sk == 0) return DGG_OK;
+  DGG_REQUIRE(q && k, DGG_ERR_NULL, "%s: null q/k pointer", op);
+  DGG_REQUIRE(dgg::aligned16(q) && dgg::aligned16(k), DGG_ERR_ALIGN, "%s: q/k must be 16-byte aligned", op);
+  return DGG_OK;
+}
+
+AttnParams make_params(const void* q, const void* k, const void* v, void* o, int64_t B, int64_t Sq, int64_t Sk,
+                       int64_t Hq, int64_t Hkv, float scale, float softcap, int64_t window, uint32_t flags) {
+  AttnParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.o = o;
+  p.B = (int)B;
+  p.Sq = (int)Sq;
+  p.Sk = (int)Sk;
+  p.Hq = (int)Hq;
+  p.Hkv = (int)Hkv;
+  p.group = (int)(Hq / Hkv);
+  p.causal = (flags & DGG_ATTN_CAUSAL) ? 1 : 0;
+  p.window = (int)window;
+  p.offset = (int)(Sk - Sq);
+  p.scale = scale;
+  p.ref_div = (float)(1.0 / (double)scale);
+  p.c_fast = scale * kLog2e;
+  p.softcap = softcap;
+  p.inv_softcap = softcap > 0.f ? 1.0f / softcap : 0.f;
+  p.sc_a = softcap > 0.f ? 2.0f * scale / softcap * kLog2e : 0.f;
+  p.sc_b = softcap * kLog2e;
+  return p;
+}
+
+}  // namespace
+
+extern "C" int dgg_attn_prefill(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B,
+                                int64_t Sq, int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides,
+                                float scale, float softcap, int64_t window, uint32_t flags, int dtype, void* stream) {
+  if (int rc = validate_attn("attn_prefill", q, k, B, Sq, Sk, Hq, Hkv, D, strides, 12, scale, softcap, window, dtype))
+    return rc;
+  if (B == 0 || Sq == 0) return DGG_OK;
+  DGG_REQUIRE(v && o, DGG_ERR_NULL, "attn_prefill: null v/o pointer");
+  DGG_REQUIRE(dgg::aligned16(v) && dgg::aligned16(o), DGG_ERR_ALIGN, "attn_prefill: v/o must be 16-byte aligned");
+  AttnParams p = make_params(q, k, v, o, B, Sq, Sk, Hq, Hkv, scale, softcap, window, flags);
+  p.lse = lse;
+  p.q_sb = strides[0]; p.q_ss = strides[1]; p.q_sh = strides[2];
+  p.k_sb = strides[3]; p.k_ss = strides[4]; p.k_sh = strides[5];
+  p.v_sb = strides[6]; p.v_ss = strides[7]; p.v_sh = strides[8];
+  p.o_sb = strides[9]; p.o_ss = strides[10]; p.o_sh = strides[11];
+  p.n_tiles = (int)((Sq + kBM - 1) / kBM);
+  const bool ref = (flags & DGG_ATTN_REF_ROUNDING) != 0;
+  hipStream_t st = dgg::as_stream(stream);
+  // Sk == 0 still launches: with no key tiles every row ends fully masked (o NaN, lse -inf), like any
+  // other row that sees no key.
+  if (dtype == DGG_BF16) {
+    if (D == 64) pick_fwd<BF16, 64>(p, ref, st);
+    else if (D == 128) pick_fwd<BF16, 128>(p, ref, st);
+    else pick_fwd<BF16, 256>(p, ref, st);
+  } else {
+    if (D == 64) pick_fwd<F16, 64>(p, ref, st);
+    else if (D == 128) pick_fwd<F16, 128>(p, ref, st);
+    else pick_fwd<F16, 256>(p, ref, st);
+  }
+  return dgg::check_launch("attn_prefill");
+}
+
+extern "C" int dgg_attn_colsum(const void* q, const void* k, const float* lse, float* colsum, int64_t B, int64_t Sq,
+                               int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides, float scale,
+                               float softcap, int64_t window, uint32_t flags, int dtype, void* stream) {
+  if (int rc = validate_attn("attn_colsum", q, k, B, Sq, Sk, Hq, Hkv, D, strides, 6, scale, softcap, window, dtype))
+    return rc;
+  if (B == 0 || Sk == 0) return DGG_OK;
+  DGG_REQUIRE(colsum != nullptr, DGG_ERR_NULL, "attn_colsum: null colsum pointer");
+  DGG_REQUIRE(Sq == 0 || lse != nullptr, DGG_ERR_NULL, "attn_colsum: null lse pointer");
+  AttnParams p = make_params(q, k, nullptr, nullptr, B, Sq, Sk, Hq, Hkv, scale, softcap, window, flags);
+  p.lse = const_cast<float*>(lse);
+  p.colsum = colsum;
+  p.q_sb = strides[0]; p.q_ss = strides[1]; p.q_sh = strides[2];
+  p.k_sb = strides[3]; p.k_ss = strides[4]; p.k_sh = strides[5];
+  p.n_tiles = (int)((Sk + kCBK - 1) / kCBK);
+  const bool ref = (flags & DGG_ATTN_REF_ROUNDING) != 0;
+  hipStream_t st = dgg::as_stream(stream);
+  if (dtype == DGG_BF16) {
+    if (D == 64) pick_col<BF16, 64>(p, ref, st);
+    else if (D == 128) pick_col<BF16, 128>(p, ref, st);
+    else pick_col<BF16, 256>(p, ref, st);
+  } else {
+    if (D == 64) pick_col<F16, 64>(p, ref, st);
+    else if (D == 128) pick_col<F16, 128>(p, ref, st);
+    else pick_col<F16, 256>(p, ref, st);
+  }
+  return dgg::check_launch("attn_colsum");
+}

@@ -1,0 +1,334 @@
+// Decode attention (one query token per sequence) as split-KV + log-sum-exp merge, and the H2O top-k.
+//
+// Decode is HBM-bound: each (batch, head, split) workgroup streams its slice of the K and V caches once
+// with 16-byte loads. Lanes are grouped D/8 per key row, so one wave instruction covers 512/D whole
+// key rows (1 KiB contiguous per wave); the four waves of a workgroup interleave rows so that one
+// iteration of the workgroup reads 2 KiB..4 KiB of contiguous cache. Each lane group keeps its own
+// online-softmax state (max, sum, 8 output columns) in registers; the 4*512/D states of a workgroup are
+// merged once through LDS into the split's partial (unnormalised output, max, sum) in the workspace.
+// A second small kernel merges the splits of each (batch, head).
+#include <algorithm>
+
+#include "common.h"
+
+namespace {
+
+constexpr int kDecThreads = 256;
+constexpr int kUnroll = 8;  // key rows per lane group per block (loads in flight per lane: 2 * kUnroll)
+
+struct DecodeParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;
+  float* part_o;   // [B, Hq, splits, D]
+  float* part_ml;  // [B, Hq, splits, 2]
+  int64_t q_sb, q_sh;
+  int64_t k_sb, k_sh, k_sl;
+  int64_t v_sb, v_sh, v_sl;
+  int64_t o_sb, o_sh;
+  int B, Hq, Hkv, group, L, splits, chunk;
+  float c;  // scale * log2(e)
+};
+
+template <typename T, int D>
+__global__ void __launch_bounds__(kDecThreads) decode_partial_kernel(DecodeParams p) {
+  typedef typename T::scalar S;
+  typedef typename T::vec8 V8;
+  constexpr int LPK = D / 8;                 // lanes per key row
+  constexpr int GPW = 64 / LPK;              // key rows per wave instruction
+  constexpr int GROUPS = GPW * (kDecThreads / 64);  // lane groups per workgroup
+  __shared__ float sm[GROUPS], sl[GROUPS];
+  __shared__ float so[GROUPS][D + 4];
+
+  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int hk = h / p.group;
+  const int tid = threadIdx.x;
+  const int grp = tid / LPK;  // 0..GROUPS-1 (row slot inside one workgroup iteration)
+  const int sub = tid % LPK;  // which 8 head-dim elements
+  const int k0 = split * p.chunk;
+  const int k1 = min(p.L, k0 + p.chunk);
+
+  const S* qp = static_cast<const S*>(p.q) + b * p.q_sb + h * p.q_sh;
+  const S* kp = static_cast<const S*>(p.k) + b * p.k_sb + hk * p.k_sh + sub * 8;
+  const S* vp = static_cast<const S*>(p.v) + b * p.v_sb + hk * p.v_sh + sub * 8;
+  f32x8 qv = to_f32x8(ld16<V8>(qp + sub * 8)) * p.c;
+
+  float m = -INFINITY, l = 0.f;
+  f32x8 acc = {};
+  for (int base = k0; base < k1; base += GROUPS * kUnroll) {
+    V8 kr[kUnroll], vr[kUnroll];
+    bool ok[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int key = base + u * GROUPS + grp;
+      ok[u] = key < k1;
+      kr[u] = ok[u] ? ld16<V8>(kp + (int64_t)key * p.k_sl) : V8{};
+      vr[u] = ok[u] ? ld16<V8>(vp + (int64_t)key * p.v_sl) : V8{};
+    }
+    float s[kUnroll];
+    float bm = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const f32x8 kf = to_f32x8(kr[u]);
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d = fmaf(qv[e], kf[e], d);
+#pragma unroll
+      for (int off = LPK / 2; off >= 1; off >>= 1) d += __shfl_xor(d, off, 64);
+      s[u] = ok[u] ? d : -INFINITY;
+      bm = fmaxf(bm, s[u]);
+    }
+    const float m_new = fmaxf(m, bm);
+    if (m_new > m) {
+      const float alpha = fast_exp2(m - m_new);  // m == -inf -> 0
+      l *= alpha;
+      acc *= alpha;
+      m = m_new;
+    }
+    const float mu = m == -INFINITY ? 0.f : m;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const float pe = fast_exp2(s[u] - mu);
+      l += pe;
+      acc += pe * to_f32x8(vr[u]);
+    }
+  }
+
+  // Merge the lane groups of the workgroup through LDS.
+  if (sub == 0) {
+    sm[grp] = m;
+    sl[grp] = l;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) so[grp][sub * 8 + e] = acc[e];
+  __syncthreads();
+  float M = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < GROUPS; ++i) M = fmaxf(M, sm[i]);
+  const float Mu = M == -INFINITY ? 0.f : M;
+  const int64_t pidx = ((int64_t)b * p.Hq + h) * p.splits + split;
+  for (int d = tid; d < D; d += kDecThreads) {
+    float od = 0.f;
+#pragma unroll
+    for (int i = 0; i < GROUPS; ++i) od += fast_exp2(sm[i] - Mu) * so[i][d];
+    p.part_o[pidx * D + d] = od;
+  }
+  if (tid == 0) {
+    float L = 0.f;
+#pragma unroll
+    for (int i = 0; i < GROUPS; ++i) L += fast_exp2(sm[i] - Mu) * sl[i];
+    p.part_ml[pidx * 2 + 0] = M;
+    p.part_ml[pidx * 2 + 1] = L;
+  }
+}
+
+// Merge: o = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s, lse = (M + log2 L) ln 2.
+template <typename T, int D>
+__global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams p) {
+  typedef typename T::scalar S;
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int64_t base = ((int64_t)b * p.Hq + h) * p.splits;
+  __shared__ float red[8];
+  float M = -INFINITY;
+  for (int s = threadIdx.x; s < p.splits; s += blockDim.x) M = fmaxf(M, p.part_ml[(base + s) * 2]);
+  M = wave_max(M);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = M;
+  __syncthreads();
+  M = -INFINITY;
+  for (int i = 0; i < (int)(blockDim.x + 63) / 64; ++i) M = fmaxf(M, red[i]);
+  const float Mu = M == -INFINITY ? 0.f : M;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float od = 0.f, L = 0.f;
+    for (int s = 0; s < p.splits; ++s) {
+      const float wgt = fast_exp2(p.part_ml[(base + s) * 2] - Mu);
+      L += wgt * p.part_ml[(base + s) * 2 + 1];
+      od += wgt * p.part_o[(base + s) * D + d];
+    }
+    static_cast<S*>(p.o)[b * p.o_sb + h * p.o_sh + d] = to_s<S>(od / L);
+    if (d == 0 && p.lse != nullptr) p.lse[(int64_t)b * p.Hq + h] = (M == -INFINITY ? -INFINITY : M + fast_log2(L)) * kLn2;
+  }
+}
+
+template <typename T, int D>
+void launch_decode(const DecodeParams& p, hipStream_t st) {
+  hipLaunchKernelGGL((decode_partial_kernel<T, D>), dim3(p.splits, p.Hq, p.B), dim3(kDecThreads), 0, st, p);
+  hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(p.Hq, p.B), dim3(D < 256 ? 128 : 256), 0, st, p);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Top-k with lowest-index tie-break (one 1024-thread workgroup per row). Radix select over an
+// order-preserving 32-bit key (4 passes of 8 bits) finds the k-th largest key K*; every element with
+// key > K* is taken, plus the lowest-indexed elements equal to K* until k are taken. Each thread owns a
+// contiguous index segment, so block-wide exclusive scans give both the tie ranks and the output
+// positions in ascending index order.
+// ------------------------------------------------------------------------------------------------
+constexpr int kTopkThreads = 1024;
+
+__device__ __forceinline__ uint32_t order_key(float x) {
+  uint32_t u = __float_as_uint(x == 0.f ? 0.f : x);  // -0.0 == +0.0
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Block-wide exclusive scan of one uint32 per thread (1024 threads = 16 waves).
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wsum, uint32_t& total) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  uint32_t inc = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t t = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += t;
+  }
+  if (lane == 63) wsum[wid] = inc;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+  for (int i = 0; i < kTopkThreads / 64; ++i) {
+    const uint32_t s = wsum[i];
+    if (i < wid) before += s;
+    all += s;
+  }
+  __syncthreads();
+  total = all;
+  return before + inc - v;
+}
+
+__global__ void __launch_bounds__(kTopkThreads) topk_kernel(const float* __restrict__ scores, int n, int k,
+                                                             int64_t* __restrict__ out) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t wsum[kTopkThreads / 64];
+  __shared__ uint32_t sel_digit, sel_remaining;
+  const float* x = scores + (int64_t)blockIdx.x * n;
+  int64_t* o = out + (int64_t)blockIdx.x * k;
+  const int tid = threadIdx.x;
+  const int per = (n + kTopkThreads - 1) / kTopkThreads;
+  const int seg0 = min(n, tid * per), seg1 = min(n, seg0 + per);
+
+  uint32_t prefix = 0, pmask = 0, remaining = (uint32_t)k;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = tid; i < 256; i += kTopkThreads) hist[i] = 0;
+    __syncthreads();
+    for (int i = seg0; i < seg1; ++i) {
+      const uint32_t key = order_key(x[i]);
+      if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t cum = 0;
+      int dsel = 0;
+      for (int d = 255; d >= 0; --d) {
+        if (cum + hist[d] >= remaining) {
+          dsel = d;
+          break;
+        }
+        cum += hist[d];
+      }
+      sel_digit = (uint32_t)dsel;
+      sel_remaining = remaining - cum;
+    }
+    __syncthreads();
+    prefix |= sel_digit << shift;
+    pmask |= 255u << shift;
+    remaining = sel_remaining;
+    __syncthreads();
+  }
+  // prefix = K*; `remaining` elements equal to K* are still to be taken, lowest index first.
+  uint32_t eq = 0;
+  for (int i = seg0; i < seg1; ++i) eq += order_key(x[i]) == prefix;
+  uint32_t tot;
+  const uint32_t eq_before = block_exclusive_scan(eq, wsum, tot);
+  uint32_t sel = 0, eq_seen = eq_before;
+  for (int i = seg0; i < seg1; ++i) {
+    const uint32_t key = order_key(x[i]);
+    if (key > prefix) ++sel;
+    else if (key == prefix) sel += (eq_seen++ < remaining);
+  }
+  const uint32_t pos0 = block_exclusive_scan(sel, wsum, tot);
+  uint32_t pos = pos0;
+  eq_seen = eq_before;
+  for (int i = seg0; i < seg1; ++i) {
+    const uint32_t key = order_key(x[i]);
+    bool take = key > prefix;
+    if (key == prefix) take = eq_seen++ < remaining;
+    if (take && pos < (uint32_t)k) o[pos++] = i;
+  }
+}
+
+}  // namespace
+
+extern "C" int64_t dgg_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t splits) {
+  if (B < 0 || Hq < 0 || D < 0 || splits < 0) return -1;
+  return B * Hq * splits * (D + 2) * (int64_t)sizeof(float);
+}
+
+extern "C" int dgg_attn_decode(const void* q, const void* k, const void* v, void* o, float* lse, void* workspace,
+                               int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
+                               const int64_t* strides, int64_t splits, float scale, int dtype, void* stream) {
+  const char* op = "attn_decode";
+  DGG_REQUIRE(dtype == DGG_F16 || dtype == DGG_BF16, DGG_ERR_DTYPE,
+              "%s: dtype code %d not supported (attention kernels take f16 or bf16)", op, dtype);
+  DGG_REQUIRE(D == 64 || D == 128 || D == 256, DGG_ERR_UNSUPPORTED, "%s: head_dim %lld not supported (64, 128, 256)",
+              op, (long long)D);
+  DGG_REQUIRE(B >= 0 && B < 65536 && Hq > 0 && Hq < 65536 && Hkv > 0 && Hq % Hkv == 0, DGG_ERR_SHAPE,
+              "%s: bad batch/head sizes (B=%lld Hq=%lld Hkv=%lld)", op, (long long)B, (long long)Hq, (long long)Hkv);
+  DGG_REQUIRE(L >= 1 && L < (1ll << 31), DGG_ERR_SHAPE, "%s: kv length must be in [1, 2^31) (got %lld)", op,
+              (long long)L);
+  DGG_REQUIRE(splits >= 1 && splits <= 1024, DGG_ERR_SHAPE, "%s: splits must be in [1, 1024] (got %lld)", op,
+              (long long)splits);
+  DGG_REQUIRE(std::isfinite(scale) && scale > 0.f, DGG_ERR_SHAPE, "%s: scale must be finite and > 0", op);
+  DGG_REQUIRE(strides != nullptr, DGG_ERR_NULL, "%s: strides is NULL", op);
+  for (int i = 0; i < 10; ++i)
+    DGG_REQUIRE(strides[i] >= 0 && strides[i] % 8 == 0, DGG_ERR_STRIDE,
+                "%s: stride[%d] = %lld must be a non-negative multiple of 8 elements", op, i, (long long)strides[i]);
+  const int64_t need = dgg_attn_decode_workspace_bytes(B, Hq, D, splits);
+  DGG_REQUIRE(workspace_bytes >= need, DGG_ERR_WORKSPACE, "%s: workspace of %lld bytes < required %lld", op,
+              (long long)workspace_bytes, (long long)need);
+  if (B == 0) return DGG_OK;
+  DGG_REQUIRE(q && k && v && o && workspace, DGG_ERR_NULL, "%s: null pointer", op);
+  DGG_REQUIRE(dgg::aligned16(q) && dgg::aligned16(k) && dgg::aligned16(v) && dgg::aligned16(workspace),
+              DGG_ERR_ALIGN, "%s: q/k/v/workspace must be 16-byte aligned", op);
+  DecodeParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.o = o;
+  p.lse = lse;
+  p.part_o = static_cast<float*>(workspace);
+  p.part_ml = p.part_o + B * Hq * splits * D;
+  p.q_sb = strides[0]; p.q_sh = strides[1];
+  p.k_sb = strides[2]; p.k_sh = strides[3]; p.k_sl = strides[4];
+  p.v_sb = strides[5]; p.v_sh = strides[6]; p.v_sl = strides[7];
+  p.o_sb = strides[8]; p.o_sh = strides[9];
+  p.B = (int)B;
+  p.Hq = (int)Hq;
+  p.Hkv = (int)Hkv;
+  p.group = (int)(Hq / Hkv);
+  p.L = (int)L;
+  p.splits = (int)splits;
+  p.chunk = (int)((L + splits - 1) / splits);
+  p.c = scale * kLog2e;
+  hipStream_t st = dgg::as_stream(stream);
+  if (dtype == DGG_BF16) {
+    if (D == 64) launch_decode<BF16, 64>(p, st);
+    else if (D == 128) launch_decode<BF16, 128>(p, st);
+    else launch_decode<BF16, 256>(p, st);
+  } else {
+    if (D == 64) launch_decode<F16, 64>(p, st);
+    else if (D == 128) launch_decode<F16, 128>(p, st);
+    else launch_decode<F16, 256>(p, st);
+  }
+  return dgg::check_launch(op);
+}
+
+extern "C" int dgg_topk_indices(const float* scores, int64_t rows, int64_t n, int64_t k, int64_t* out_idx,
+                                void* stream) {
+  DGG_REQUIRE(rows >= 0 && rows < (1ll << 31), DGG_ERR_SHAPE, "topk_indices: bad row count %lld", (long long)rows);
+  DGG_REQUIRE(n >= 1 && n <= 65536, DGG_ERR_SHAPE, "topk_indices: n must be in [1, 65536] (got %lld)", (long long)n);
+  DGG_REQUIRE(k >= 1 && k <= n, DGG_ERR_SHAPE, "topk_indices: k must be in [1, n] (got k=%lld, n=%lld)",
+              (long long)k, (long long)n);
+  if (rows == 0) return DGG_OK;
+  DGG_REQUIRE(scores && out_idx, DGG_ERR_NULL, "topk_indices: null pointer");
+  hipLaunchKernelGGL(topk_kernel, dim3((unsigned)rows), dim3(kTopkThreads), 0, dgg::as_stream(stream), scores, (int)n,
+                     (int)k, out_idx);
+  return dgg::check_launch("topk_indices");
+}

@@ -1,0 +1,393 @@
+// Elementwise kernels of the Llama layer around attention: RMSNorm, fused residual-add + RMSNorm,
+// SiLU-and-mul and online rotary embedding. All are HBM-bound: 16-byte vector loads/stores, one pass
+// over the data (the row of an RMSNorm is held in registers between the reduction and the scaling),
+// fp32 arithmetic, and rounding to the storage type at the points where the reference rounds.
+#include "common.h"
+
+namespace {
+
+// Vector traits: a 16-byte chunk holds EPV elements.
+template <typename T>
+struct VecOf;
+template <>
+struct VecOf<F16> {
+  typedef f16x8 type;
+  static constexpr int EPV = 8;
+};
+template <>
+struct VecOf<BF16> {
+  typedef bf16x8 type;
+  static constexpr int EPV = 8;
+};
+template <>
+struct VecOf<F32> {
+  typedef f32x4 type;
+  static constexpr int EPV = 4;
+};
+
+template <typename T>
+__device__ __forceinline__ float round_t(float x) {
+  return to_f<typename T::scalar>(to_s<typename T::scalar>(x));
+}
+template <>
+__device__ __forceinline__ float round_t<F32>(float x) {
+  return x;
+}
+
+// Block-wide sum for up to 1024 threads (wave64 shuffles, then one LDS hop).
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int nw = (blockDim.x + 63) >> 6;
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float t = lane < nw ? red[lane] : 0.f;
+  t = wave_sum(t);
+  return t;
+}
+
+// ---------------------------------------------------------------------------------------------
+// RMSNorm (csrc/norm.cu:34-56). Vector path: the row is read once into registers (NV chunks per thread).
+// RESID: fused residual add (csrc/norm.cu:59-83): v = in + res; res = T(v); variance from the unrounded v;
+// output from the rounded residual.
+// ---------------------------------------------------------------------------------------------
+template <typename T, int NV, bool RESID>
+__global__ void __launch_bounds__(1024) rms_norm_vec_kernel(typename T::scalar* __restrict__ out,
+                                                             const typename T::scalar* __restrict__ in,
+                                                             typename T::scalar* __restrict__ res,
+                                                             const typename T::scalar* __restrict__ w,
+                                                             int hidden, int64_t in_rs, int64_t out_rs,
+                                                             int64_t res_rs, float eps) {
+  typedef typename VecOf<T>::type V;
+  constexpr int EPV = VecOf<T>::EPV;
+  __shared__ float red[16];
+  const int64_t row = blockIdx.x;
+  const int nvec = hidden / EPV;
+  const typename T::scalar* x = in + row * in_rs;
+  float vals[NV][EPV];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = threadIdx.x + i * blockDim.x;
+    if (c < nvec) {
+      V a = ld16<V>(x + (int64_t)c * EPV);
+      if constexpr (RESID) {
+        typename T::scalar* r = res + row * res_rs + (int64_t)c * EPV;
+        V b = ld16<V>(r);
+        V rr;
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+          float v = to_f(a[e]) + to_f(b[e]);
+          ss += v * v;
+          rr[e] = to_s<typename T::scalar>(v);
+          vals[i][e] = to_f(rr[e]);
+        }
+        st16<V>(r, rr);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+          float v = to_f(a[e]);
+          vals[i][e] = v;
+          ss += v * v;
+        }
+      }
+    }
+  }
+  ss = block_sum(ss, red);
+  const float s = rsqrtf(ss / (float)hidden + eps);
+  typename T::scalar* y = out + row * out_rs;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = threadIdx.x + i * blockDim.x;
+    if (c < nvec) {
+      V wv = ld16<V>(w + (int64_t)c * EPV);
+      V o;
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) o[e] = to_s<typename T::scalar>(round_t<T>(vals[i][e] * s) * to_f(wv[e]));
+      st16<V>(y + (int64_t)c * EPV, o);
+    }
+  }
+}
+
+// Scalar fallback for any hidden size / alignment: two passes over the row (second pass re-reads it).
+template <typename T, bool RESID>
+__global__ void __launch_bounds__(1024) rms_norm_scalar_kernel(typename T::scalar* __restrict__ out,
+                                                                const typename T::scalar* __restrict__ in,
+                                                                typename T::scalar* __restrict__ res,
+                                                                const typename T::scalar* __restrict__ w,
+                                                                int hidden, int64_t in_rs, int64_t out_rs,
+                                                                int64_t res_rs, float eps) {
+  __shared__ float red[16];
+  const int64_t row = blockIdx.x;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < hidden; i += blockDim.x) {
+    float v = to_f(in[row * in_rs + i]);
+    if constexpr (RESID) {
+      v += to_f(res[row * res_rs + i]);
+      res[row * res_rs + i] = to_s<typename T::scalar>(v);
+    }
+    ss += v * v;
+  }
+  ss = block_sum(ss, red);
+  const float s = rsqrtf(ss / (float)hidden + eps);
+  for (int i = threadIdx.x; i < hidden; i += blockDim.x) {
+    float v = RESID ? to_f(res[row * res_rs + i]) : to_f(in[row * in_rs + i]);
+    out[row * out_rs + i] = to_s<typename T::scalar>(round_t<T>(v * s) * to_f(w[i]));
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// SiLU-and-mul (csrc/activation.cu:6-22): out = T(T(silu(g)) * u), silu in fp32.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ float silu_f(float g) { return g * fast_rcp(1.f + fast_exp2(-g * kLog2e)); }
+
+template <typename T>
+__global__ void __launch_bounds__(256) silu_and_mul_vec_kernel(typename T::scalar* __restrict__ out,
+                                                                const typename T::scalar* __restrict__ in,
+                                                                int64_t rows, int64_t d, int64_t in_rs,
+                                                                int64_t out_rs) {
+  typedef typename VecOf<T>::type V;
+  constexpr int EPV = VecOf<T>::EPV;
+  const int64_t vpr = d / EPV;
+  const int64_t total = rows * vpr;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = t / vpr, c = (t - r * vpr) * EPV;
+    const typename T::scalar* src = in + r * in_rs;
+    V g = ld16<V>(src + c);
+    V u = ld16<V>(src + d + c);
+    V o;
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) o[e] = to_s<typename T::scalar>(round_t<T>(silu_f(to_f(g[e]))) * to_f(u[e]));
+    st16<V>(out + r * out_rs + c, o);
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) silu_and_mul_scalar_kernel(typename T::scalar* __restrict__ out,
+                                                                   const typename T::scalar* __restrict__ in,
+                                                                   int64_t rows, int64_t d, int64_t in_rs,
+                                                                   int64_t out_rs) {
+  const int64_t total = rows * d;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = t / d, c = t - r * d;
+    float g = to_f(in[r * in_rs + c]);
+    float u = to_f(in[r * in_rs + d + c]);
+    out[r * out_rs + c] = to_s<typename T::scalar>(round_t<T>(silu_f(g)) * u);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Online rotary (csrc/pos_encoding.cu:64-113). One workgroup per token: the D/2 (cos, sin) pairs are
+// computed once into LDS with accurate powf / sincosf (angles reach thousands of radians), then every
+// (head, 8-pair group) of q and k is rotated with 16-byte loads. VEC=false: scalar element path.
+// ---------------------------------------------------------------------------------------------
+template <typename T, bool VEC>
+__global__ void __launch_bounds__(256) rotary_online_kernel(const int32_t* __restrict__ pos,
+                                                             typename T::scalar* __restrict__ q,
+                                                             typename T::scalar* __restrict__ k, int hq,
+                                                             int hk, int D, int64_t q_rs, int64_t k_rs,
+                                                             float theta) {
+  __shared__ float cs[256], sn[256];
+  const int half = D / 2;
+  const int64_t tok = blockIdx.x;
+  const float p = (float)pos[tok];
+  for (int i = threadIdx.x; i < half; i += blockDim.x) {
+    const float ang = p / powf(theta, (float)(2 * i) / (float)D);
+    float s, c;
+    sincosf(ang, &s, &c);
+    cs[i] = c;
+    sn[i] = s;
+  }
+  __syncthreads();
+  if constexpr (VEC) {
+    typedef typename VecOf<T>::type V;
+    constexpr int EPV = VecOf<T>::EPV;
+    const int gph = half / EPV;  // pair groups per head
+    const int items = (hq + hk) * gph;
+    for (int it = threadIdx.x; it < items; it += blockDim.x) {
+      const int h = it / gph, gi = it - h * gph;
+      typename T::scalar* base = h < hq ? q + tok * q_rs + (int64_t)h * D : k + tok * k_rs + (int64_t)(h - hq) * D;
+      const int i0 = gi * EPV;
+      V x = ld16<V>(base + i0), y = ld16<V>(base + half + i0);
+      V xo, yo;
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) {
+        const float c = cs[i0 + e], s = sn[i0 + e];
+        const float xf = to_f(x[e]), yf = to_f(y[e]);
+        xo[e] = to_s<typename T::scalar>(xf * c - yf * s);
+        yo[e] = to_s<typename T::scalar>(yf * c + xf * s);
+      }
+      st16<V>(base + i0, xo);
+      st16<V>(base + half + i0, yo);
+    }
+  } else {
+    const int items = (hq + hk) * half;
+    for (int it = threadIdx.x; it < items; it += blockDim.x) {
+      const int h = it / half, i = it - h * half;
+      typename T::scalar* base = h < hq ? q + tok * q_rs + (int64_t)h * D : k + tok * k_rs + (int64_t)(h - hq) * D;
+      const float xf = to_f(base[i]), yf = to_f(base[half + i]);
+      const float c = cs[i], s = sn[i];
+      base[i] = to_s<typename T::scalar>(xf * c - yf * s);
+      base[half + i] = to_s<typename T::scalar>(yf * c + xf * s);
+    }
+  }
+}
+
+template <typename T, int NV, bool RESID>
+void launch_rms_vec(int threads, void* out, const void* in, void* res, const void* w, int64_t rows, int hidden,
+                    int64_t in_rs, int64_t out_rs, int64_t res_rs, float eps, hipStream_t st) {
+  typedef typename T::scalar S;
+  hipLaunchKernelGGL((rms_norm_vec_kernel<T, NV, RESID>), dim3((unsigned)rows), dim3(threads), 0, st, (S*)out,
+                     (const S*)in, (S*)res, (const S*)w, hidden, in_rs, out_rs, res_rs, eps);
+}
+
+template <typename T, bool RESID>
+int rms_dispatch(void* out, const void* in, void* res, const void* w, int64_t rows, int64_t hidden, int64_t in_rs,
+                 int64_t out_rs, int64_t res_rs, float eps, hipStream_t st) {
+  typedef typename T::scalar S;
+  constexpr int EPV = VecOf<T>::EPV;
+  const bool vec = hidden % EPV == 0 && in_rs % EPV == 0 && out_rs % EPV == 0 && (!RESID || res_rs % EPV == 0) &&
+                   dgg::aligned16(out) && dgg::aligned16(in) && dgg::aligned16(w) && (!RESID || dgg::aligned16(res));
+  const int64_t nvec = hidden / EPV;
+  if (vec && nvec <= 8 * 1024) {
+    int threads = (int)((nvec + 63) / 64 * 64);
+    if (threads > 256) threads = 256;
+    const int64_t per = (nvec + threads - 1) / threads;
+    if (per > 8) {
+      threads = (int)(((nvec + 7) / 8 + 63) / 64 * 64);  // <= 1024 for nvec <= 8192
+    }
+    const int64_t nv = (nvec + threads - 1) / threads;
+    if (nv <= 1) launch_rms_vec<T, 1, RESID>(threads, out, in, res, w, rows, (int)hidden, in_rs, out_rs, res_rs, eps, st);
+    else if (nv <= 2) launch_rms_vec<T, 2, RESID>(threads, out, in, res, w, rows, (int)hidden, in_rs, out_rs, res_rs, eps, st);
+    else if (nv <= 4) launch_rms_vec<T, 4, RESID>(threads, out, in, res, w, rows, (int)hidden, in_rs, out_rs, res_rs, eps, st);
+    else launch_rms_vec<T, 8, RESID>(threads, out, in, res, w, rows, (int)hidden, in_rs, out_rs, res_rs, eps, st);
+  } else {
+    const int threads = hidden >= 1024 ? 1024 : (int)((hidden + 63) / 64 * 64);
+    hipLaunchKernelGGL((rms_norm_scalar_kernel<T, RESID>), dim3((unsigned)rows), dim3(threads), 0, st, (S*)out,
+                       (const S*)in, (S*)res, (const S*)w, (int)hidden, in_rs, out_rs, res_rs, eps);
+  }
+  return dgg::check_launch(RESID ? "fused_add_rms_norm" : "rms_norm");
+}
+
+template <typename T>
+int silu_dispatch(void* out, const void* in, int64_t rows, int64_t d, int64_t in_rs, int64_t out_rs, hipStream_t st) {
+  typedef typename T::scalar S;
+  constexpr int EPV = VecOf<T>::EPV;
+  const bool vec = d % EPV == 0 && in_rs % EPV == 0 && out_rs % EPV == 0 && dgg::aligned16(out) && dgg::aligned16(in);
+  const int64_t work = vec ? rows * (d / EPV) : rows * d;
+  int64_t blocks = (work + 255) / 256;
+  if (blocks > 256 * 64) blocks = 256 * 64;
+  if (vec)
+    hipLaunchKernelGGL((silu_and_mul_vec_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, st, (S*)out, (const S*)in,
+                       rows, d, in_rs, out_rs);
+  else
+    hipLaunchKernelGGL((silu_and_mul_scalar_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, st, (S*)out,
+                       (const S*)in, rows, d, in_rs, out_rs);
+  return dgg::check_launch("silu_and_mul");
+}
+
+template <typename T>
+int rotary_dispatch(const int32_t* pos, void* q, void* k, int64_t tokens, int64_t hq, int64_t hk, int64_t D,
+                    int64_t q_rs, int64_t k_rs, float theta, hipStream_t st) {
+  typedef typename T::scalar S;
+  constexpr int EPV = VecOf<T>::EPV;
+  const bool vec = (D / 2) % EPV == 0 && q_rs % EPV == 0 && (k == nullptr || k_rs % EPV == 0) && dgg::aligned16(q) &&
+                   (k == nullptr || dgg::aligned16(k));
+  const int64_t items = (hq + hk) * (vec ? D / 2 / EPV : D / 2);
+  int threads = (int)((items + 63) / 64 * 64);
+  if (threads > 256) threads = 256;
+  if (threads < 64) threads = 64;
+  if (vec)
+    hipLaunchKernelGGL((rotary_online_kernel<T, true>), dim3((unsigned)tokens), dim3(threads), 0, st, pos, (S*)q,
+                       (S*)k, (int)hq, (int)hk, (int)D, q_rs, k_rs, theta);
+  else
+    hipLaunchKernelGGL((rotary_online_kernel<T, false>), dim3((unsigned)tokens), dim3(threads), 0, st, pos, (S*)q,
+                       (S*)k, (int)hq, (int)hk, (int)D, q_rs, k_rs, theta);
+  return dgg::check_launch("rotary_embedding_online");
+}
+
+int check_rows(const char* op, int64_t rows, int64_t cols, int64_t in_rs, int64_t out_rs, int64_t min_in_rs) {
+  DGG_REQUIRE(rows >= 0, DGG_ERR_SHAPE, "%s: rows must be >= 0 (got %lld)", op, (long long)rows);
+  DGG_REQUIRE(rows <= 0x7fffffff, DGG_ERR_SHAPE, "%s: rows must be < 2^31 (got %lld)", op, (long long)rows);
+  DGG_REQUIRE(cols > 0, DGG_ERR_SHAPE, "%s: row width must be > 0 (got %lld)", op, (long long)cols);
+  DGG_REQUIRE(cols <= 0x7fffffff, DGG_ERR_SHAPE, "%s: row width must be < 2^31 (got %lld)", op, (long long)cols);
+  DGG_REQUIRE(in_rs >= min_in_rs, DGG_ERR_STRIDE, "%s: input row stride %lld is smaller than the row (%lld)", op,
+              (long long)in_rs, (long long)min_in_rs);
+  DGG_REQUIRE(out_rs >= cols, DGG_ERR_STRIDE, "%s: output row stride %lld is smaller than the row (%lld)", op,
+              (long long)out_rs, (long long)cols);
+  return DGG_OK;
+}
+
+}  // namespace
+
+extern "C" int dgg_rms_norm(void* out, const void* input, const void* weight, int64_t rows, int64_t hidden,
+                            int64_t in_row_stride, int64_t out_row_stride, int dtype, float epsilon, void* stream) {
+  DGG_REQUIRE(dgg::valid_dtype(dtype), DGG_ERR_DTYPE, "rms_norm: unsupported dtype code %d", dtype);
+  if (int rc = check_rows("rms_norm", rows, hidden, in_row_stride, out_row_stride, hidden)) return rc;
+  if (rows == 0) return DGG_OK;
+  DGG_REQUIRE(out && input && weight, DGG_ERR_NULL, "rms_norm: null pointer");
+  hipStream_t st = dgg::as_stream(stream);
+  switch (dtype) {
+    case DGG_F16: return rms_dispatch<F16, false>(out, input, nullptr, weight, rows, hidden, in_row_stride, out_row_stride, 0, epsilon, st);
+    case DGG_BF16: return rms_dispatch<BF16, false>(out, input, nullptr, weight, rows, hidden, in_row_stride, out_row_stride, 0, epsilon, st);
+    default: return rms_dispatch<F32, false>(out, input, nullptr, weight, rows, hidden, in_row_stride, out_row_stride, 0, epsilon, st);
+  }
+}
+
+extern "C" int dgg_fused_add_rms_norm(void* input, void* residual, const void* weight, int64_t rows, int64_t hidden,
+                                      int64_t in_row_stride, int64_t res_row_stride, int dtype, float epsilon,
+                                      void* stream) {
+  DGG_REQUIRE(dgg::valid_dtype(dtype), DGG_ERR_DTYPE, "fused_add_rms_norm: unsupported dtype code %d", dtype);
+  if (int rc = check_rows("fused_add_rms_norm", rows, hidden, in_row_stride, in_row_stride, hidden)) return rc;
+  DGG_REQUIRE(res_row_stride >= hidden, DGG_ERR_STRIDE, "fused_add_rms_norm: residual row stride %lld < hidden %lld",
+              (long long)res_row_stride, (long long)hidden);
+  if (rows == 0) return DGG_OK;
+  DGG_REQUIRE(input && residual && weight, DGG_ERR_NULL, "fused_add_rms_norm: null pointer");
+  hipStream_t st = dgg::as_stream(stream);
+  switch (dtype) {
+    case DGG_F16: return rms_dispatch<F16, true>(input, input, residual, weight, rows, hidden, in_row_stride, in_row_stride, res_row_stride, epsilon, st);
+    case DGG_BF16: return rms_dispatch<BF16, true>(input, input, residual, weight, rows, hidden, in_row_stride, in_row_stride, res_row_stride, epsilon, st);
+    default: return rms_dispatch<F32, true>(input, input, residual, weight, rows, hidden, in_row_stride, in_row_stride, res_row_stride, epsilon, st);
+  }
+}
+
+extern "C" int dgg_silu_and_mul(void* out, const void* input, int64_t rows, int64_t d, int64_t in_row_stride,
+                                int64_t out_row_stride, int dtype, void* stream) {
+  DGG_REQUIRE(dgg::valid_dtype(dtype), DGG_ERR_DTYPE, "silu_and_mul: unsupported dtype code %d", dtype);
+  if (int rc = check_rows("silu_and_mul", rows, d, in_row_stride, out_row_stride, 2 * d)) return rc;
+  if (rows == 0) return DGG_OK;
+  DGG_REQUIRE(out && input, DGG_ERR_NULL, "silu_and_mul: null pointer");
+  hipStream_t st = dgg::as_stream(stream);
+  switch (dtype) {
+    case DGG_F16: return silu_dispatch<F16>(out, input, rows, d, in_row_stride, out_row_stride, st);
+    case DGG_BF16: return silu_dispatch<BF16>(out, input, rows, d, in_row_stride, out_row_stride, st);
+    default: return silu_dispatch<F32>(out, input, rows, d, in_row_stride, out_row_stride, st);
+  }
+}
+
+extern "C" int dgg_rotary_embedding_online(const int32_t* positions, void* query, void* key, int64_t tokens,
+                                           int64_t head_num, int64_t kv_head_num, int64_t head_dim,
+                                           int64_t q_row_stride, int64_t k_row_stride, int dtype, float rope_theta,
+                                           void* stream) {
+  DGG_REQUIRE(dgg::valid_dtype(dtype), DGG_ERR_DTYPE, "rotary_embedding_online: unsupported dtype code %d", dtype);
+  DGG_REQUIRE(head_dim > 0 && head_dim % 16 == 0 && head_dim <= 512, DGG_ERR_UNSUPPORTED,
+              "rotary_embedding_online: head_dim must be a positive multiple of 16 up to 512 (got %lld)",
+              (long long)head_dim);
+  DGG_REQUIRE(tokens >= 0 && tokens <= 0x7fffffff, DGG_ERR_SHAPE, "rotary_embedding_online: bad token count %lld",
+              (long long)tokens);
+  DGG_REQUIRE(head_num > 0 && kv_head_num >= 0 && head_num + kv_head_num <= 65536, DGG_ERR_SHAPE,
+              "rotary_embedding_online: bad head counts %lld / %lld", (long long)head_num, (long long)kv_head_num);
+  DGG_REQUIRE(q_row_stride >= head_num * head_dim, DGG_ERR_STRIDE,
+              "rotary_embedding_online: query row stride %lld < head_num*head_dim", (long long)q_row_stride);
+  if (key == nullptr) kv_head_num = 0;
+  DGG_REQUIRE(kv_head_num == 0 || k_row_stride >= kv_head_num * head_dim, DGG_ERR_STRIDE,
+              "rotary_embedding_online: key row stride %lld < kv_head_num*head_dim", (long long)k_row_stride);
+  if (tokens == 0) return DGG_OK;
+  DGG_REQUIRE(positions && query, DGG_ERR_NULL, "rotary_embedding_online: null pointer");
+  hipStream_t st = dgg::as_stream(stream);
+  switch (dtype) {
+    case DGG_F16: return rotary_dispatch<F16>(positions, query, key, tokens, head_num, kv_head_num, head_dim, q_row_stride, k_row_stride, rope_theta, st);
+    case DGG_BF16: return rotary_dispatch<BF16>(positions, query, key, tokens, head_num, kv_head_num, head_dim, q_row_stride, k_row_stride, rope_theta, st);
+    default: return rotary_dispatch<F32>(positions, query, key, tokens, head_num, kv_head_num, head_dim, q_row_stride, k_row_stride, rope_theta, st);
+  }
+}

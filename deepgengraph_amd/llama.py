@@ -1,0 +1,55 @@
+"""Llama-2 glue around the attention kernels: the config-2 attention block and the config-5 decode step.
+
+The attention block follows LlamaLayer.forward's first half (deepgengraph_exp/cases/models/attn.py:71-74) and
+Attention.forward (models/attn.py:34-53): RMSNorm -> fused QKV projection -> rotary on q and k -> causal
+attention -> output projection. The projections are plain library GEMMs (torch.matmul -> hipBLASLt); everything
+else runs in libdgg_hip.so. Unlike the reference, q/k/v are not copied out of the QKV result with
+.contiguous() (models/attn.py:36-39): the rotary and attention kernels take the strided views directly.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import attention as _attn
+from . import ops
+
+
+class LlamaAttentionBlock:
+    def __init__(self, w_norm, w_qkv, w_o, *, heads: int, kv_heads: int, eps: float = 1e-6,
+                 rope_theta: float = 10000.0):
+        self.w_norm, self.w_qkv, self.w_o = w_norm, w_qkv, w_o
+        self.heads, self.kv_heads = heads, kv_heads
+        self.hidden = w_o.shape[0]
+        self.head_dim = self.hidden // heads
+        self.eps, self.theta = eps, rope_theta
+        self._pos = None
+
+    def positions(self, B: int, S: int, device) -> torch.Tensor:
+        """Token positions 0..S-1 (models/attn.py:40), repeated for each batch entry."""
+        if self._pos is None or self._pos.shape != (B, S) or self._pos.device != device:
+            self._pos = torch.arange(S, dtype=torch.int32, device=device).repeat(B, 1).contiguous()
+        return self._pos
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        B, S, _ = x.shape
+        D, H, Hk = self.head_dim, self.heads, self.kv_heads
+        h = torch.empty_like(x)
+        ops.rms_norm(h, x, self.w_norm, self.eps)                      # LlamaLayer.input_layernorm
+        qkv = torch.matmul(h, self.w_qkv.t())                          # models/attn.py:35
+        q = qkv[..., : H * D]
+        k = qkv[..., H * D: (H + Hk) * D]
+        v = qkv[..., (H + Hk) * D:]
+        ops.rotary_embedding_online(self.positions(B, S, x.device), q, k, D, self.theta)  # models/attn.py:41
+        o = _attn.attention(q.view(B, S, H, D), k.view(B, S, Hk, D), v.view(B, S, Hk, D), causal=True)
+        return torch.matmul(o.view(B, S, H * D), self.w_o.t())         # models/attn.py:52
+
+
+def decode_prestep(x: torch.Tensor, w_norm: torch.Tensor, gate_up: torch.Tensor, eps: float = 1e-6):
+    """Config 5 pre-step: RMSNorm of the query-side hidden state and SiLU-and-mul of the MLP activation pair
+    (LlamaLayer's RmsNorm.forward and MLP.forward elementwise parts, llama_base.py:287-289, 305-314).
+    Returns (normed, act)."""
+    normed = torch.empty_like(x)
+    ops.rms_norm(normed, x, w_norm, eps)
+    act = torch.empty(*gate_up.shape[:-1], gate_up.shape[-1] // 2, dtype=gate_up.dtype, device=gate_up.device)
+    ops.silu_and_mul(act, gate_up)
+    return normed, act

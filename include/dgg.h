@@ -1,0 +1,132 @@
+/*
+ * dgg.h - C ABI of libdgg_hip.so, the MI355X (gfx950) kernels of the DeepGenGraph attention hot path.
+ *
+ * Every entry point:
+ *   - takes raw device pointers, sizes and element strides (no framework types),
+ *   - never allocates or frees device memory (scratch is passed in by the caller),
+ *   - validates every argument on the host before anything is launched,
+ *   - launches asynchronously on the given hipStream_t (passed as void*; NULL = default stream),
+ *   - returns DGG_OK (0) or a negative DGG_ERR_* code; the message of the last failure on the
+ *     calling thread is returned by dgg_last_error().
+ *
+ * dtype codes follow the order of the reference's dispatch macro
+ * (csrc/utils.h:3-8: Float, Half, BFloat16).
+ */
+#ifndef DGG_H_
+#define DGG_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DGG_ABI_VERSION 1
+
+enum dgg_dtype { DGG_F32 = 0, DGG_F16 = 1, DGG_BF16 = 2 };
+
+enum dgg_status {
+  DGG_OK = 0,
+  DGG_ERR_DTYPE = -1,       /* dtype not supported by this op */
+  DGG_ERR_SHAPE = -2,       /* a size is negative, zero where it must not be, or inconsistent */
+  DGG_ERR_STRIDE = -3,      /* innermost stride is not 1, or a stride is not a multiple of the vector width */
+  DGG_ERR_ALIGN = -4,       /* a pointer is not aligned to the vector width */
+  DGG_ERR_UNSUPPORTED = -5, /* head_dim / option combination without a kernel */
+  DGG_ERR_LAUNCH = -6,      /* hipGetLastError() reported a failure after the launch */
+  DGG_ERR_NULL = -7,        /* a required pointer is NULL */
+  DGG_ERR_WORKSPACE = -8    /* caller-provided scratch is too small */
+};
+
+/* Flags for the attention entry points. */
+#define DGG_ATTN_CAUSAL 0x1u /* bottom-right aligned causal mask: key j is visible to query i iff j <= i + (Sk - Sq) */
+/* Round scores to the input dtype at the points where the reference's eager module rounds them
+ * (Q.K^T result, the 1/sqrt(D) scaling, each soft-cap step) before the fp32 softmax. Costs a few VALU
+ * ops per score; used where downstream selection (H2O top-k) depends on exact probabilities. */
+#define DGG_ATTN_REF_ROUNDING 0x2u
+
+int dgg_abi_version(void);
+const char* dgg_last_error(void);
+
+/* ---------------------------------------------------------------------------------------------
+ * Elementwise ops: replace the pybind11 module of csrc/ffi.cpp:4-8 (prototypes csrc/op.h:2-6).
+ * Rows are [rows, hidden]; strides are in elements between consecutive rows; columns are contiguous.
+ * ------------------------------------------------------------------------------------------- */
+
+/* csrc/norm.cu:85-98 rms_norm(out, input, weight, epsilon):
+ *   out[r,i] = T( T(x[r,i] * rsqrt(mean_i x[r,i]^2 + eps)) * w[i] ), fp32 accumulation.
+ * weight has the input dtype (csrc/norm.cu:96). out may alias input. */
+int dgg_rms_norm(void* out, const void* input, const void* weight, int64_t rows, int64_t hidden,
+                 int64_t in_row_stride, int64_t out_row_stride, int dtype, float epsilon, void* stream);
+
+/* csrc/norm.cu:100-113 fused_add_rms_norm(input, residual, weight, epsilon), in place:
+ *   residual = T(input + residual);  input = rms_norm(residual).  (Not exported by the reference's
+ *   ffi.cpp; provided for the Llama layer's residual + norm pair.) */
+int dgg_fused_add_rms_norm(void* input, void* residual, const void* weight, int64_t rows, int64_t hidden,
+                           int64_t in_row_stride, int64_t res_row_stride, int dtype, float epsilon,
+                           void* stream);
+
+/* csrc/activation.cu:24-34 silu_and_mul(out, input): input [rows, 2d] = [gate | up],
+ *   out[r,i] = T( T(silu(gate[r,i])) * up[r,i] ). */
+int dgg_silu_and_mul(void* out, const void* input, int64_t rows, int64_t d, int64_t in_row_stride,
+                     int64_t out_row_stride, int dtype, void* stream);
+
+/* csrc/pos_encoding.cu:180-199 rotary_embedding_online(positions, query, key, head_size, rope_theta):
+ * NeoX pairing (i, i + D/2), angle = pos / theta^(2i/D) in fp32, in place on query [tokens, head_num*D]
+ * and key [tokens, kv_head_num*D] with row strides q_row_stride / k_row_stride.
+ * The reference asserts D == 128 (pos_encoding.cu:195); this build accepts any even D that is a
+ * multiple of 16 up to 512 and returns DGG_ERR_UNSUPPORTED otherwise. key may be NULL (Q only). */
+int dgg_rotary_embedding_online(const int32_t* positions, void* query, void* key, int64_t tokens,
+                                int64_t head_num, int64_t kv_head_num, int64_t head_dim, int64_t q_row_stride,
+                                int64_t k_row_stride, int dtype, float rope_theta, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Attention. The reference has no kernel ABI for attention: it is the callable returned by
+ * compile(model, input_names, inputs, output_names, system) (compile.py:6,296) that runs
+ * Attn.forward / Gemma2.forward / H2O.forward (deepgengraph_exp/cases/kernels/{attn,gemma2,h2o}.py).
+ * These entry points are what that callable launches here.
+ *
+ * Layout: q [B, Sq, Hq, D], k/v [B, Sk, Hkv, D], o [B, Sq, Hq, D] (the case modules' layout), given as
+ * element strides {batch, seq, head} with the D stride fixed at 1. Hq must be a multiple of Hkv
+ * (query head h reads KV head h / (Hq/Hkv)). dtype: DGG_F16 or DGG_BF16. D in {64, 128, 256}.
+ * ------------------------------------------------------------------------------------------- */
+
+/* Fused online-softmax attention forward.
+ *   scores = (q . k^T) * scale; if softcap > 0: scores = softcap * tanh(scores / softcap);
+ *   mask (flags & DGG_ATTN_CAUSAL: key j visible iff j <= i + Sk - Sq; window > 0: also iff
+ *   i + Sk - Sq - j < window); p = softmax_j(scores) in fp32; o = p . v.
+ * lse (optional, may be NULL): fp32 [B, Hq, Sq] contiguous, natural-log log-sum-exp of the masked
+ * scaled scores; -inf for a row with no visible key (its o row is NaN, as the reference's softmax of an
+ * all -inf row). strides: 12 int64 = q{b,s,h}, k{b,s,h}, v{b,s,h}, o{b,s,h}. */
+int dgg_attn_prefill(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t Sq,
+                     int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides, float scale,
+                     float softcap, int64_t window, uint32_t flags, int dtype, void* stream);
+
+/* H2O column sums (deepgengraph_exp/cases/kernels/h2o.py:35-36): colsum[b,h,j] = sum_i p[b,h,i,j] with p
+ * the fp32 probabilities of dgg_attn_prefill, recomputed from q, k and the lse it wrote (same scale,
+ * softcap, window and flags). colsum: fp32 [B, Hq, Sk] contiguous. strides: 6 int64 = q{b,s,h}, k{b,s,h}. */
+int dgg_attn_colsum(const void* q, const void* k, const float* lse, float* colsum, int64_t B, int64_t Sq,
+                    int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides, float scale,
+                    float softcap, int64_t window, uint32_t flags, int dtype, void* stream);
+
+/* Top-k of H2O scores (deepgengraph_exp/cases/models/h2o.py:51-52: torch.topk then sort of the indices):
+ * for each of `rows` rows of n fp32 scores (row stride n), the k largest, ties broken by the lowest index,
+ * written as int64 indices in ascending index order to out_idx [rows, k]. -0.0 equals +0.0; NaN is not
+ * supported. n <= 65536. */
+int dgg_topk_indices(const float* scores, int64_t rows, int64_t n, int64_t k, int64_t* out_idx, void* stream);
+
+/* Decode attention (Attn.forward with q_len == 1, attn.py:22-23: no mask) as split-KV + LSE merge.
+ * q [B, Hq, D] strides {b,h}; k/v cache [B, Hkv, L, D] strides {b,h,l}; o [B, Hq, D] strides {b,h}.
+ * strides: 10 int64 = q{b,h}, k{b,h,l}, v{b,h,l}, o{b,h}.
+ * workspace: fp32 scratch of dgg_attn_decode_workspace_bytes(B, Hq, D, splits) bytes, 16B aligned:
+ * per (b, h, split) the unnormalised partial output, its max and its sum.
+ * lse (optional): fp32 [B, Hq], natural log. splits in [1, 1024]; L >= 1. */
+int64_t dgg_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t splits);
+int dgg_attn_decode(const void* q, const void* k, const void* v, void* o, float* lse, void* workspace,
+                    int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
+                    const int64_t* strides, int64_t splits, float scale, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DGG_H_ */

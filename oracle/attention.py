@@ -1,0 +1,164 @@
+"""CPU restatement of the reference attention cases — TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+All functions take CPU tensors in the case layout [B, S, H, D] (decode: q [B, H, D], cache [B, H, L, D]) and
+evaluate the reference's eager PyTorch formula with its rounding points:
+
+  scores = (q @ k^T) / sqrt(D)          in the input dtype (matmul result rounded, then the division rounded)
+  soft-cap: scores /= c; tanh; *= c     each step in the input dtype (gemma2.py:31-33)
+  scores += mask                        -inf / 0 in the input dtype; adding 0 is exact, so masked_fill is used
+  probs = softmax(scores.float())       fp32
+  out = probs.to(dtype) @ v             input dtype
+
+Query rows are processed in chunks: softmax is per row, so chunking changes nothing but peak memory.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+
+def _mask(i0: int, n: int, Sq: int, Sk: int, causal: bool, window: int | None) -> torch.Tensor | None:
+    """Boolean [n, Sk] mask of *hidden* pairs for query rows i0..i0+n.
+
+    causal: attn.py:22-23 builds triu(full(-inf), diagonal = Sk - Sq + 1), i.e. key j is hidden from query i
+    iff j > i + (Sk - Sq) (bottom-right aligned; q_len == 1 hides nothing).
+    window (extension for the Gemma-2-style config): key j is also hidden iff i + (Sk - Sq) - j >= window.
+    """
+    if not causal and not window:
+        return None
+    i = torch.arange(i0, i0 + n).unsqueeze(1) + (Sk - Sq)
+    j = torch.arange(Sk).unsqueeze(0)
+    hidden = torch.zeros(n, Sk, dtype=torch.bool)
+    if causal:
+        hidden |= j > i
+    if window:
+        hidden |= (i - j) >= window
+    return hidden
+
+
+def attention(q, k, v, *, causal=True, softcap=None, window=None, return_lse=False, q_chunk=256):
+    """Attn.forward (deepgengraph_exp/cases/kernels/attn.py:18-34) and Gemma2.forward (gemma2.py:19-38).
+
+    Extensions used by the BASELINE configs: GQA with query head h reading KV head h // (Hq // Hkv) (the
+    expand/reshape convention of roco.py:25-27) and an optional causal sliding window.
+    Returns out [B, Sq, Hq, D] in q.dtype, and with return_lse the natural-log log-sum-exp [B, Hq, Sq] (fp32)
+    of the masked fp32 scores that the softmax sees (-inf for a row with no visible key).
+    """
+    B, Sq, Hq, D = q.shape
+    Sk, Hkv = k.shape[1], k.shape[2]
+    assert Hq % Hkv == 0
+    group = Hq // Hkv
+    dt = q.dtype
+    qt = q.transpose(1, 2)  # attn.py:25-27
+    kt = k.transpose(1, 2)
+    vt = v.transpose(1, 2)
+    if group > 1:
+        kt = kt.repeat_interleave(group, dim=1)
+        vt = vt.repeat_interleave(group, dim=1)
+    kT = kt.transpose(-2, -1)
+    out = torch.empty(B, Hq, Sq, D, dtype=dt)
+    lse = torch.empty(B, Hq, Sq, dtype=torch.float32) if return_lse else None
+    for i0 in range(0, Sq, q_chunk):
+        n = min(q_chunk, Sq - i0)
+        scores = torch.matmul(qt[:, :, i0:i0 + n], kT) / math.sqrt(D)  # attn.py:29
+        if softcap:
+            scores /= softcap  # gemma2.py:31-33
+            scores = torch.tanh(scores)
+            scores *= softcap
+        hidden = _mask(i0, n, Sq, Sk, causal, window)
+        if hidden is not None:
+            scores = scores.masked_fill(hidden, float("-inf"))  # attn.py:30 (`scores += mask`)
+        sf = scores.float()
+        probs = torch.softmax(sf, dim=-1)  # attn.py:31
+        out[:, :, i0:i0 + n] = torch.matmul(probs.to(dt), vt)  # attn.py:32
+        if return_lse:
+            lse[:, :, i0:i0 + n] = torch.logsumexp(sf, dim=-1)
+    out = out.transpose(1, 2).contiguous()  # attn.py:32-34
+    return (out, lse) if return_lse else out
+
+
+def h2o(q, k, v, *, q_chunk=256):
+    """H2O.forward (deepgengraph_exp/cases/kernels/h2o.py:18-38): causal attention plus the fp32 column sums of
+    the fp32 probabilities over the query axis, h2o_score [B, H, Sk] (h2o.py:35-36; MHA, as h2o.py:16 asserts).
+    Returns (out, h2o_score, lse)."""
+    B, Sq, Hq, D = q.shape
+    Sk, Hkv = k.shape[1], k.shape[2]
+    assert Hq == Hkv, "H2O is multi-head attention (h2o.py:16)"
+    dt = q.dtype
+    qt, kt, vt = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    kT = kt.transpose(-2, -1)
+    out = torch.empty(B, Hq, Sq, D, dtype=dt)
+    lse = torch.empty(B, Hq, Sq, dtype=torch.float32)
+    colsum = torch.zeros(B, Hq, Sk, dtype=torch.float32)
+    for i0 in range(0, Sq, q_chunk):
+        n = min(q_chunk, Sq - i0)
+        scores = torch.matmul(qt[:, :, i0:i0 + n], kT) / math.sqrt(D)  # h2o.py:29
+        scores = scores.masked_fill(_mask(i0, n, Sq, Sk, True, None), float("-inf"))  # h2o.py:30
+        sf = scores.float()
+        probs = torch.softmax(sf, dim=-1)  # h2o.py:31
+        out[:, :, i0:i0 + n] = torch.matmul(probs.to(dt), vt)  # h2o.py:32
+        colsum += probs.sum(dim=2)  # h2o.py:35-36
+        lse[:, :, i0:i0 + n] = torch.logsumexp(sf, dim=-1)
+    return out.transpose(1, 2).contiguous(), colsum, lse
+
+
+def decode(q, k_cache, v_cache):
+    """Attn.forward with q_len == 1 (attn.py:18-34): the mask triu(diagonal = L) hides nothing (attn.py:22-23).
+
+    q [B, Hq, D]; k_cache / v_cache [B, Hkv, L, D] (the module's post-transpose layout); out [B, Hq, D].
+    Also returns the natural-log LSE [B, Hq] of the fp32 scores. Processed one batch entry at a time."""
+    B, Hq, D = q.shape
+    Hkv = k_cache.shape[1]
+    group = Hq // Hkv
+    dt = q.dtype
+    out = torch.empty(B, Hq, D, dtype=dt)
+    lse = torch.empty(B, Hq, dtype=torch.float32)
+    for b in range(B):
+        kb, vb = k_cache[b], v_cache[b]
+        if group > 1:
+            kb = kb.repeat_interleave(group, dim=0)
+            vb = vb.repeat_interleave(group, dim=0)
+        scores = torch.matmul(q[b].unsqueeze(1), kb.transpose(-2, -1)) / math.sqrt(D)  # [Hq, 1, L]
+        sf = scores.float()
+        probs = torch.softmax(sf, dim=-1)
+        out[b] = torch.matmul(probs.to(dt), vb).squeeze(1)
+        lse[b] = torch.logsumexp(sf, dim=-1).squeeze(1)
+    return out, lse
+
+
+def decode_splitkv(q, k_cache, v_cache, splits: int, scale: float | None = None):
+    """Split-KV decode + log-sum-exp merge in float64 (numpy). No reference counterpart: it is pinned by being
+    equal to the unsplit softmax for every split count. Per split s over keys [s*c, (s+1)*c), c = ceil(L/splits):
+    m_s = max x, l_s = sum exp(x - m_s), O_s = sum exp(x - m_s) v; merge: M = max m_s,
+    o = sum e^(m_s - M) O_s / sum e^(m_s - M) l_s, lse = M + log(sum e^(m_s - M) l_s)."""
+    qn = q.double().numpy()
+    kn = k_cache.double().numpy()
+    vn = v_cache.double().numpy()
+    B, Hq, D = qn.shape
+    Hkv, L = kn.shape[1], kn.shape[2]
+    group = Hq // Hkv
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    c = -(-L // splits)
+    out = np.zeros((B, Hq, D))
+    lse = np.zeros((B, Hq))
+    for b in range(B):
+        for h in range(Hq):
+            x = kn[b, h // group] @ qn[b, h] * scale
+            ms, ls, os_ = [], [], []
+            for s in range(splits):
+                xs = x[s * c:(s + 1) * c]
+                if xs.size == 0:
+                    continue
+                m = xs.max()
+                p = np.exp(xs - m)
+                ms.append(m)
+                ls.append(p.sum())
+                os_.append(p @ vn[b, h // group, s * c:(s + 1) * c])
+            M = max(ms)
+            wts = np.exp(np.array(ms) - M)
+            lt = float((wts * np.array(ls)).sum())
+            out[b, h] = (wts[:, None] * np.array(os_)).sum(0) / lt
+            lse[b, h] = M + math.log(lt)
+    return out, lse

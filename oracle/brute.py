@@ -1,0 +1,117 @@
+"""Float64 pure-Python loops over tiny inputs: the independent pins of the oracle — TEST INFRASTRUCTURE ONLY.
+
+These follow the mathematical definitions (no intermediate rounding, math.exp / math.sin / math.cos in float64),
+written without torch so that a mistake in the vectorised oracle (a wrong mask diagonal, a transposed operand,
+a wrong GQA head, a dropped scale) shows up as a mismatch. Inputs are nested lists or numpy arrays.
+"""
+from __future__ import annotations
+
+import math
+
+
+def attention(q, k, v, *, causal=True, softcap=None, window=None, scale=None):
+    """q [B][Sq][Hq][D], k/v [B][Sk][Hkv][D] -> (out [B][Sq][Hq][D], lse [B][Hq][Sq]).
+    Key j visible to query i iff (not causal or j <= i + Sk - Sq) and (not window or i + Sk - Sq - j < window);
+    query head h reads KV head h // (Hq // Hkv)."""
+    B, Sq, Hq, D = len(q), len(q[0]), len(q[0][0]), len(q[0][0][0])
+    Sk, Hkv = len(k[0]), len(k[0][0])
+    group = Hq // Hkv
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    off = Sk - Sq
+    out = [[[[0.0] * D for _ in range(Hq)] for _ in range(Sq)] for _ in range(B)]
+    lse = [[[0.0] * Sq for _ in range(Hq)] for _ in range(B)]
+    for b in range(B):
+        for h in range(Hq):
+            hk = h // group
+            for i in range(Sq):
+                xs = []
+                for j in range(Sk):
+                    if causal and j > i + off:
+                        continue
+                    if window and i + off - j >= window:
+                        continue
+                    s = sum(float(q[b][i][h][d]) * float(k[b][j][hk][d]) for d in range(D)) * scale
+                    if softcap:
+                        s = softcap * math.tanh(s / softcap)
+                    xs.append((j, s))
+                if not xs:
+                    out[b][i][h] = [float("nan")] * D
+                    lse[b][h][i] = float("-inf")
+                    continue
+                m = max(s for _, s in xs)
+                den = sum(math.exp(s - m) for _, s in xs)
+                lse[b][h][i] = m + math.log(den)
+                for d in range(D):
+                    out[b][i][h][d] = sum(math.exp(s - m) * float(v[b][j][hk][d]) for j, s in xs) / den
+    return out, lse
+
+
+def colsum(q, k, *, causal=True, scale=None):
+    """H2O column sums: colsum[b][h][j] = sum_i softmax_j(scores_i)[j] (h2o.py:35-36), float64."""
+    B, Sq, Hq, D = len(q), len(q[0]), len(q[0][0]), len(q[0][0][0])
+    Sk, Hkv = len(k[0]), len(k[0][0])
+    group = Hq // Hkv
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    off = Sk - Sq
+    cs = [[[0.0] * Sk for _ in range(Hq)] for _ in range(B)]
+    for b in range(B):
+        for h in range(Hq):
+            for i in range(Sq):
+                xs = [(j, sum(float(q[b][i][h][d]) * float(k[b][j][h // group][d]) for d in range(D)) * scale)
+                      for j in range(Sk) if not (causal and j > i + off)]
+                if not xs:
+                    continue
+                m = max(s for _, s in xs)
+                den = sum(math.exp(s - m) for _, s in xs)
+                for j, s in xs:
+                    cs[b][h][j] += math.exp(s - m) / den
+    return cs
+
+
+def rms_norm(x, w, eps):
+    """Rows of x: y_i = x_i / sqrt(mean(x^2) + eps) * w_i (csrc/norm.cu:34-56 without rounding)."""
+    out = []
+    for row in x:
+        ms = sum(float(a) * float(a) for a in row) / len(row)
+        s = 1.0 / math.sqrt(ms + eps)
+        out.append([float(a) * s * float(wi) for a, wi in zip(row, w)])
+    return out
+
+
+def silu_and_mul(x):
+    """Rows [g | u]: g / (1 + e^-g) * u (csrc/activation.cu:6-22 without rounding)."""
+    out = []
+    for row in x:
+        d = len(row) // 2
+        out.append([float(row[i]) / (1.0 + math.exp(-float(row[i]))) * float(row[d + i]) for i in range(d)])
+    return out
+
+
+def rotary(pos, x, head_dim, theta):
+    """Rows of x ([T][H*D]) rotated per head: pairs (i, i + D/2), angle pos / theta^(2i/D) (float64)."""
+    half = head_dim // 2
+    out = []
+    for p, row in zip(pos, x):
+        o = list(map(float, row))
+        for h in range(len(row) // head_dim):
+            base = h * head_dim
+            for i in range(half):
+                a = float(p) / theta ** (2.0 * i / head_dim)
+                c, s = math.cos(a), math.sin(a)
+                xa, ya = float(row[base + i]), float(row[base + half + i])
+                o[base + i] = xa * c - ya * s
+                o[base + half + i] = ya * c + xa * s
+        out.append(o)
+    return out
+
+
+def topk_indices(row, k):
+    """Definition by exhaustive ranking: element i outranks j iff x_i > x_j or (x_i == x_j and i < j);
+    the k elements outranked by fewer than k others, in ascending index order."""
+    n = len(row)
+    sel = []
+    for i in range(n):
+        rank = sum(1 for j in range(n) if row[j] > row[i] or (row[j] == row[i] and j < i))
+        if rank < k:
+            sel.append(i)
+    return sel

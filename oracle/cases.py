@@ -1,0 +1,62 @@
+"""The reference's attention case modules restated on the CPU oracle — TEST INFRASTRUCTURE ONLY.
+
+Same class names, constructor arguments and attributes as deepgengraph_exp/cases/kernels/{attn,gemma2,h2o}.py,
+so that tests can hand them to deepgengraph_amd.compile.compile() exactly as run_kernel.py:44-78 does. forward()
+evaluates the oracle (oracle/attention.py) on CPU copies of the inputs and returns CPU tensors.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import attention as _oa
+
+
+class _Case(nn.Module):
+    def __init__(self, kv_head_num=32, head_num=32, head_dim=128):
+        super().__init__()
+        self.kv_head_num = kv_head_num
+        self.head_num = head_num
+        self.head_dim = head_dim
+        self.hidden_size = head_num * head_dim
+        self.kv_hidden_size = kv_head_num * head_dim
+        self.group_size = self.head_num // self.kv_head_num
+
+    def prepare(self, batch_size=1, q_len=4096, kv_len=4096, dtype=torch.float16, device="cpu", seed=0):
+        """attn.py:36-50 / gemma2.py:41-54 / h2o.py:41-55, with randn inputs from a seeded CPU generator."""
+        g = torch.Generator().manual_seed(seed)
+        q = torch.randn(batch_size, q_len, self.head_num, self.head_dim, generator=g).to(dtype).to(device)
+        k = torch.randn(batch_size, kv_len, self.kv_head_num, self.head_dim, generator=g).to(dtype).to(device)
+        v = torch.randn(batch_size, kv_len, self.kv_head_num, self.head_dim, generator=g).to(dtype).to(device)
+        return {"input": {"q": q, "k": k, "v": v}, "output": list(self.OUTPUTS)}
+
+
+class Attn(_Case):
+    """deepgengraph_exp/cases/kernels/attn.py:7-34."""
+    OUTPUTS = ("out",)
+
+    def forward(self, q, k, v):
+        return _oa.attention(q.cpu(), k.cpu(), v.cpu(), causal=True)
+
+
+class Gemma2(_Case):
+    """deepgengraph_exp/cases/kernels/gemma2.py:7-38 (+ optional `sliding_window`, + GQA)."""
+    OUTPUTS = ("out",)
+
+    def __init__(self, logit_softcapping=50.0, kv_head_num=32, head_num=32, head_dim=128, sliding_window=0):
+        super().__init__(kv_head_num, head_num, head_dim)
+        self.logit_softcapping = logit_softcapping
+        self.sliding_window = sliding_window
+
+    def forward(self, q, k, v):
+        return _oa.attention(q.cpu(), k.cpu(), v.cpu(), causal=True, softcap=self.logit_softcapping,
+                             window=self.sliding_window or None)
+
+
+class H2O(_Case):
+    """deepgengraph_exp/cases/kernels/h2o.py:7-38."""
+    OUTPUTS = ("out", "h2o_score")
+
+    def forward(self, q, k, v):
+        out, colsum, _ = _oa.h2o(q.cpu(), k.cpu(), v.cpu())
+        return out, colsum.view(q.shape[0], self.kv_head_num, k.shape[1])

@@ -1,0 +1,93 @@
+"""Full-size parity for the five benchmark configurations (deepgengraph_amd.configs) on identical seeded inputs.
+Where the CPU oracle would take minutes at full size, a documented subset is checked against it (whole heads
+over the full sequence) and size-independent properties cover the rest."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close
+from deepgengraph_amd import attention as A
+from deepgengraph_amd import configs as C
+from deepgengraph_amd.llama import LlamaAttentionBlock, decode_prestep
+from oracle import attention as oa
+from oracle import elementwise as oe
+from oracle import llama as ol
+from oracle import selection as osel
+
+pytestmark = pytest.mark.gpu
+
+
+def test_config2_attention_full(gpu):
+    cfg = C.CFG2
+    q, k, v, _ = C.attn_inputs(cfg)
+    ref = oa.attention(q, k, v, causal=True)
+    out = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), causal=True)
+    assert_close(out.cpu().float(), ref.float(), 2e-2, 1e-2, "config 2 attention (all 32 heads)")
+
+
+def test_config2_block_full(gpu):
+    inp = C.llama_block_inputs()
+    ref, parts = ol.attention_block(inp["x"], inp["w_norm"], inp["w_qkv"], inp["w_o"], heads=32, kv_heads=32,
+                                    eps=C.LLAMA_EPS, theta=C.LLAMA_THETA, return_parts=True)
+    blk = LlamaAttentionBlock(*(inp[n].to(gpu) for n in ("w_norm", "w_qkv", "w_o")), heads=32, kv_heads=32,
+                              eps=C.LLAMA_EPS, rope_theta=C.LLAMA_THETA)
+    out = blk(inp["x"].to(gpu))
+    assert_close(out.cpu().float(), ref.float(), 2e-2, 1e-2, "config 2 block output")
+
+
+def test_config3_gemma2_full_sequences(gpu):
+    cfg = C.CFG3
+    q, k, v, _ = C.attn_inputs(cfg)
+    out = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), causal=True, softcap=cfg.softcap, window=cfg.window).cpu()
+    # whole sequences of (batch 0, head 0), (batch 1, head 5), (batch 1, head 15): every query row, all 8192 keys
+    for b, h in ((0, 0), (1, 5), (1, 15)):
+        hk = h // (cfg.Hq // cfg.Hkv)
+        ref = oa.attention(q[b:b + 1, :, h:h + 1], k[b:b + 1, :, hk:hk + 1], v[b:b + 1, :, hk:hk + 1], causal=True,
+                           softcap=cfg.softcap, window=cfg.window)
+        assert_close(out[b:b + 1, :, h:h + 1].float(), ref.float(), 2e-2, 1e-2, f"config 3 b{b} h{h}")
+    assert torch.isfinite(out.float()).all()
+
+
+def test_config4_h2o_full(gpu):
+    cfg = C.CFG4
+    q, k, v, sinks = C.attn_inputs(cfg)
+    ref_out, ref_cs, _ = oa.h2o(q, k, v)
+    out, cs = A.h2o_attention(q.to(gpu), k.to(gpu), v.to(gpu))
+    assert_close(out.cpu().float(), ref_out.float(), 1e-2, 5e-3, "config 4 out")
+    csc = cs.cpu()
+    assert_close(csc, ref_cs, 1e-6, 1e-3, "config 4 colsum")
+    assert_close(csc.sum(-1), torch.full((1, cfg.Hq), float(cfg.Sq)), 0, 1e-4, "sum of colsums")
+    idx = A.topk_indices(cs, cfg.topk).cpu().numpy()
+    ref_idx = osel.topk_indices(ref_cs.numpy(), cfg.topk)
+    np.testing.assert_array_equal(idx, ref_idx)
+    # every sink key is a heavy hitter in every head
+    assert all(set(sinks.tolist()) <= set(row.tolist()) for row in idx.reshape(-1, cfg.topk))
+
+
+def test_config5_decode_full(gpu):
+    cfg = C.CFG5
+    q, kc, vc = C.decode_inputs(cfg, device=gpu)
+    out, lse = A.decode_attention(q, kc, vc, splits=cfg.splits, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    for b, h in ((0, 0), (17, 5), (40, 31), (63, 31)):
+        ref, ref_lse = oa.decode(q[b:b + 1, h:h + 1].cpu(), kc[b:b + 1, h:h + 1].cpu(), vc[b:b + 1, h:h + 1].cpu())
+        assert_close(out[b:b + 1, h:h + 1].cpu().float(), ref.float(), 1e-2, 5e-3, f"config 5 decode b{b} h{h}")
+        assert_close(lse[b:b + 1, h:h + 1].cpu(), ref_lse, 1e-3, 1e-4, f"config 5 lse b{b} h{h}")
+    del kc, vc
+    pre = C.decode_prestep_inputs(cfg)
+    normed, act = decode_prestep(*(pre[n].to(gpu) for n in ("x", "w_norm", "gate_up")), eps=C.LLAMA_EPS)
+    assert_close(normed.cpu().float(), oe.rms_norm(pre["x"], pre["w_norm"], C.LLAMA_EPS).float(), 1e-2, 5e-3,
+                 "config 5 rms_norm")
+    assert_close(act.cpu().float(), oe.silu_and_mul(pre["gate_up"]).float(), 1e-2, 5e-3, "config 5 silu_and_mul")
+
+
+def test_config_work_figures():
+    # the algorithmic work each benchmark line divides by
+    assert C.CFG2.reference_flops() == 4 * 32 * 4096 * 4096 * 128 / 2
+    assert C.CFG3.pairs_per_head() == 25_167_872
+    assert abs(C.CFG3.flops() - 824.70e9) < 0.01e9
+    assert C.CFG5.bytes() == 34_360_786_944
+    assert math.isclose(C.CFG2.scale, 1 / math.sqrt(128))

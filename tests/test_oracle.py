@@ -1,0 +1,207 @@
+"""Pins the CPU oracle (oracle/) against the float64 brute-force definitions, golden vectors, closed forms and
+invariants. No GPU needed. Each check is chosen so that a plausible mistake (wrong mask diagonal, transposed
+operand, wrong GQA head, dropped scale, wrong rotary pairing, unstable tie order) fails it."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close, load_golden
+from oracle import attention as oa
+from oracle import brute
+from oracle import elementwise as oe
+from oracle import selection as osel
+
+
+def _t(x):
+    return torch.from_numpy(np.ascontiguousarray(x))
+
+
+@pytest.mark.parametrize("name,kw", [
+    ("attn_tiny_causal_f32", dict(causal=True)),
+    ("attn_tiny_gqa_softcap_window_f32", dict(causal=True, softcap=5.0, window=5)),
+    ("attn_tiny_noncausal_f32", dict(causal=False)),
+    ("attn_d64_causal_bf16", dict(causal=True)),
+    ("attn_d64_gqa_softcap_window_bf16", dict(causal=True, softcap=5.0, window=33)),
+])
+def test_attention_matches_golden(name, kw):
+    g = load_golden(name)
+    out, lse = oa.attention(_t(g["q"]), _t(g["k"]), _t(g["v"]), return_lse=True, **kw)
+    assert_close(out, g["out"], 1e-5, 1e-5, f"{name} out")
+    assert_close(lse, g["lse"], 1e-5, 1e-5, f"{name} lse")
+
+
+def test_fully_masked_rows_are_nan_like_the_reference():
+    # Sq > Sk with bottom-right alignment: the first Sq - Sk rows see no key; softmax of an all -inf row is NaN.
+    g = load_golden("attn_tiny_causal_sq_gt_sk_f32")
+    out, lse = oa.attention(_t(g["q"]), _t(g["k"]), _t(g["v"]), return_lse=True)
+    assert torch.isnan(out[0, :4]).all() and not torch.isnan(out[0, 4:]).any()
+    assert torch.isinf(lse[0, 0, :4]).all() and (lse[0, 0, :4] < 0).all()
+    assert_close(out, g["out"], 1e-5, 1e-5, "sq>sk out")
+
+
+def test_h2o_colsum_matches_golden_and_invariant():
+    g = load_golden("attn_d64_h2o_sinks_f16")
+    q, k, v = _t(g["q"]), _t(g["k"]), _t(g["v"])
+    out, colsum, lse = oa.h2o(q, k, v)
+    assert_close(colsum, g["colsum"], 1e-6, 1e-5, "colsum")
+    assert_close(out, g["out"], 1e-5, 1e-5, "h2o out")
+    # every probability row sums to 1, so the column sums of a head add up to q_len
+    assert_close(colsum.sum(-1), torch.full((1, 2), float(q.shape[1])), 0, 1e-5, "sum of colsums")
+    # causal: the last key is seen only by the last query, so its column sum is that one probability
+    s_last = (q[0, -1].double() * k[0, -1].double()).sum(-1) / math.sqrt(q.shape[-1])  # [H]
+    assert_close(colsum[0, :, -1], torch.exp(s_last - lse[0, :, -1].double()), 1e-7, 1e-5, "last column")
+
+
+def test_attention_closed_forms():
+    torch.manual_seed(0)
+    B, S, H, D = 1, 24, 2, 16
+    v = torch.randn(B, S, H, D)
+    # q = 0: every visible score is 0 -> lse_i = ln(#visible keys) = ln(i + 1); out_i = mean of v_0..v_i
+    q = torch.zeros(B, S, H, D)
+    k = torch.randn(B, S, H, D)
+    out, lse = oa.attention(q, k, v, return_lse=True)
+    assert_close(lse[0, 0], torch.log(torch.arange(1, S + 1, dtype=torch.float64)), 1e-6, 1e-6, "lse closed form")
+    means = torch.cumsum(v, 1) / torch.arange(1, S + 1).view(1, S, 1, 1)
+    assert_close(out, means, 1e-5, 1e-5, "uniform attention")
+    # first query sees only key 0
+    q = torch.randn(B, S, H, D)
+    out = oa.attention(q, k, v)
+    assert_close(out[:, 0], v[:, 0], 1e-6, 1e-6, "causal row 0")
+
+
+def test_attention_reductions():
+    torch.manual_seed(1)
+    B, S, Hq, Hkv, D = 2, 40, 4, 2, 16
+    q, k, v = torch.randn(B, S, Hq, D), torch.randn(B, S, Hkv, D), torch.randn(B, S, Hkv, D)
+    base = oa.attention(q, k, v)
+    # GQA == explicit head repeat (roco.py:25-27 convention)
+    rep = oa.attention(q, k.repeat_interleave(2, dim=2), v.repeat_interleave(2, dim=2))
+    assert torch.equal(base, rep)
+    # window >= S reduces to causal; a huge soft-cap reduces to no soft-cap
+    assert torch.equal(oa.attention(q, k, v, window=S), base)
+    assert_close(oa.attention(q, k, v, softcap=1e6), base, 1e-5, 1e-5, "softcap->inf")
+    # query chunking is exact
+    assert_close(oa.attention(q, k, v, q_chunk=7), base, 1e-6, 1e-6, "chunking")
+    # window 1 keeps only the diagonal: out_i = v_i
+    assert_close(oa.attention(q, k, v, window=1), v.repeat_interleave(2, dim=2), 1e-6, 1e-6, "window 1")
+
+
+def test_attention_low_precision_rounding_points():
+    # bf16 oracle stays within the bf16 tolerance of the fp32 evaluation of the same (exactly representable) inputs
+    torch.manual_seed(2)
+    q, k, v = (torch.randn(1, 64, 2, 64).bfloat16() for _ in range(3))
+    lo = oa.attention(q, k, v)
+    hi = oa.attention(q.float(), k.float(), v.float())
+    assert lo.dtype == torch.bfloat16
+    assert_close(lo.float(), hi, 2e-2, 1e-2, "bf16 vs fp32")
+    assert not torch.equal(lo.float(), hi.bfloat16().float()), "scores must be rounded to bf16 before the softmax"
+
+
+def test_decode_matches_attention_and_splitkv():
+    torch.manual_seed(3)
+    B, H, Hkv, L, D = 2, 4, 2, 37, 16
+    q = torch.randn(B, H, D)
+    kc, vc = torch.randn(B, Hkv, L, D), torch.randn(B, Hkv, L, D)
+    out, lse = oa.decode(q, kc, vc)
+    # decode == Attn.forward with q_len == 1 (nothing masked) in the case layout
+    ref, ref_lse = oa.attention(q.unsqueeze(1), kc.transpose(1, 2), vc.transpose(1, 2), return_lse=True)
+    assert_close(out, ref[:, 0], 1e-6, 1e-6, "decode vs attention")
+    assert_close(lse, ref_lse[:, :, 0], 1e-6, 1e-6, "decode lse")
+    o1, l1 = oa.decode_splitkv(q, kc, vc, 1)
+    for s in (2, 3, 7, L, L + 5):
+        os_, ls_ = oa.decode_splitkv(q, kc, vc, s)
+        np.testing.assert_allclose(os_, o1, rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(ls_, l1, rtol=1e-12, atol=1e-12)
+    assert_close(out, o1, 1e-5, 1e-5, "fp32 decode vs float64 split-kv")
+    # brute force (float64 loops) pins the unsplit formula
+    bo, bl = brute.attention(q.unsqueeze(1).tolist(), kc.transpose(1, 2).tolist(), vc.transpose(1, 2).tolist(),
+                             causal=False)
+    np.testing.assert_allclose(o1, np.array(bo)[:, 0], rtol=1e-10, atol=1e-10)
+
+
+def test_rms_norm():
+    g = load_golden("rms_norm_bf16")
+    x, w = _t(g["x"]), _t(g["w"])
+    assert_close(oe.rms_norm(x, w, 1e-6), g["out"], 1e-6, 1e-6, "fp32 rms_norm vs brute")
+    got = oe.rms_norm(x.bfloat16(), w.bfloat16(), 1e-6)
+    assert got.dtype == torch.bfloat16
+    assert_close(got.float(), g["out"], 2e-2, 1e-2, "bf16 rms_norm")
+    # the two rounding points: T(x*s) then T(T * w)
+    s = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6)
+    assert torch.equal(got, ((x * s).bfloat16().float() * w).bfloat16())
+    # scale invariance and unit RMS with w = 1
+    assert_close(oe.rms_norm(x * 3.0, w, 0.0), oe.rms_norm(x, w, 0.0), 1e-6, 1e-5, "scale invariance")
+    y = oe.rms_norm(x, torch.ones_like(w), 0.0)
+    assert_close(y.pow(2).mean(-1), torch.ones(x.shape[0]), 1e-5, 1e-5, "unit rms")
+
+
+def test_fused_add_rms_norm():
+    torch.manual_seed(4)
+    x, r = torch.randn(5, 32).half(), torch.randn(5, 32).half()
+    w = (1 + 0.02 * torch.randn(32)).half()
+    out, res = oe.fused_add_rms_norm(x, r, w, 1e-6)
+    assert torch.equal(res, (x.float() + r.float()).half())
+    assert_close(out.float(), oe.rms_norm((x.float() + r.float()), w.float(), 1e-6), 1e-2, 5e-3, "fused add")
+
+
+def test_silu_and_mul():
+    g = load_golden("silu_and_mul_f16")
+    x = _t(g["x"])
+    assert_close(oe.silu_and_mul(x), g["out"], 1e-6, 1e-6, "fp32 silu vs brute")
+    h = x.half()
+    got = oe.silu_and_mul(h)
+    d = x.shape[-1] // 2
+    # library routine: torch.nn.functional.silu in fp32, rounded, times up in fp16
+    assert torch.equal(got, torch.nn.functional.silu(h[:, :d].float()).half() * h[:, d:])
+    assert float(oe.silu_and_mul(torch.zeros(1, 4))[0, 0]) == 0.0
+
+
+def test_rotary():
+    g = load_golden("rotary_d32_f32")
+    pos, x = _t(g["pos"]), _t(g["x"])
+    qo, ko = oe.rotary_embedding_online(pos, x, x[:, :32].contiguous(), 32, 10000.0)
+    # fp32 angles at positions up to 4095 carry ~1e-4 rad of rounding
+    assert_close(qo, g["out"], 2e-3, 1e-3, "rotary vs float64 brute")
+    assert_close(ko, g["out"][:, :32], 2e-3, 1e-3, "rotary key")
+    # pairing is (i, i + D/2): rotating a vector with only x_0 set moves mass to x_{D/2}
+    e = torch.zeros(1, 32)
+    e[0, 0] = 1.0
+    r, _ = oe.rotary_embedding_online(torch.tensor([1], dtype=torch.int32), e, None, 32, 10000.0)
+    assert abs(float(r[0, 16]) - math.sin(1.0)) < 1e-6 and abs(float(r[0, 0]) - math.cos(1.0)) < 1e-6
+    torch.manual_seed(5)
+    D = 128
+    q = torch.randn(3, D)
+    zero, _ = oe.rotary_embedding_online(torch.zeros(3, dtype=torch.int32), q, None, D, 10000.0)
+    assert torch.equal(zero, q)  # pos 0 is the identity
+    p = torch.tensor([5, 17, 300], dtype=torch.int32)
+    rq, _ = oe.rotary_embedding_online(p, q, None, D, 10000.0)
+    pair_norm = lambda t: t[:, : D // 2] ** 2 + t[:, D // 2:] ** 2  # noqa: E731
+    assert_close(pair_norm(rq), pair_norm(q), 1e-5, 1e-5, "pair norms")
+    # composition: rot(a) after rot(b) == rot(a + b)
+    a, b = torch.tensor([7, 9, 11], dtype=torch.int32), torch.tensor([3, 20, 100], dtype=torch.int32)
+    rab, _ = oe.rotary_embedding_online(a, oe.rotary_embedding_online(b, q, None, D, 10000.0)[0], None, D, 10000.0)
+    assert_close(rab, oe.rotary_embedding_online(a + b, q, None, D, 10000.0)[0], 1e-4, 1e-4, "composition")
+    # relative position: <rot_m q, rot_n k> depends only on m - n
+    k = torch.randn(1, D)
+    dots = []
+    for m, n in ((10, 4), (106, 100), (1006, 1000)):
+        qm, _ = oe.rotary_embedding_online(torch.tensor([m], dtype=torch.int32), q[:1], None, D, 10000.0)
+        kn, _ = oe.rotary_embedding_online(torch.tensor([n], dtype=torch.int32), k, None, D, 10000.0)
+        dots.append(float((qm * kn).sum()))
+    assert max(dots) - min(dots) < 1e-3
+
+
+def test_topk_selection():
+    g = load_golden("topk_ties")
+    got = osel.topk_indices(g["x"], 17)
+    np.testing.assert_array_equal(got, g["out"])
+    # +0.0 and -0.0 tie: the lowest indices win
+    x = np.array([[0.0, -0.0, 0.0, -0.0, 1.0]], dtype=np.float32)
+    np.testing.assert_array_equal(osel.topk_indices(x, 3), [[0, 1, 4]])
+    rng = np.random.default_rng(0)
+    for _ in range(20):
+        row = rng.integers(0, 4, size=40).astype(np.float32)
+        k = int(rng.integers(1, 40))
+        np.testing.assert_array_equal(osel.topk_indices(row[None], k)[0], brute.topk_indices(row.tolist(), k))

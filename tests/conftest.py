@@ -28,6 +28,11 @@ def gpu():
     return torch.device("cuda:0")
 
 
+def progress(msg):
+    """Progress line for long tests (visible with pytest -s)."""
+    print(f"[progress] {msg}", flush=True)
+
+
 def load_golden(name):
     import numpy as np
 

@@ -37,8 +37,9 @@ def test_rms_norm(gpu, rows, hidden, dtype):
     ops.rms_norm(out, x.to(gpu), w.to(gpu), 1e-6)
     got = out.cpu()
     assert_close(got.float(), ref.float(), *TOL[dtype], f"rms_norm {rows}x{hidden} {dtype}")
-    exact = (got == ref).float().mean().item()
-    assert exact > 0.99, f"only {exact:.4f} of elements bit-identical to the oracle"
+    if dtype != torch.float32:  # 16-bit outputs: differences only where fp32 noise crosses a rounding boundary
+        exact = (got == ref).float().mean().item()
+        assert exact > 0.99, f"only {exact:.4f} of elements bit-identical to the oracle"
 
 
 def test_rms_norm_strided_and_inplace(gpu):
@@ -122,7 +123,9 @@ def test_rotary(gpu, tokens, hq, hk, D, dtype, pad):
     g = qkv.to(gpu)
     gq, gk = g[:, : hq * D], g[:, hq * D: (hq + hk) * D]  # strided views, rotated in place
     ops.rotary_embedding_online(pos.to(gpu), gq, gk, D, 10000.0)
-    tol = TOL[dtype] if dtype != torch.float32 else (1e-4, 1e-4)
+    # fp32: the angle pos / theta^(2i/D) is itself an fp32 value (pos_encoding.cu:84); at pos ~8191 one ulp is
+    # ~5e-4 rad, so two correct fp32 evaluations (different powf) differ by up to ~1e-3 * |x| in the output.
+    tol = TOL[dtype] if dtype != torch.float32 else (3e-3, 1e-3)
     assert_close(gq.cpu().float(), ref_q.float(), *tol, "rotary q")
     assert_close(gk.cpu().float(), ref_k.float(), *tol, "rotary k")
     assert torch.equal(g[:, (hq + hk) * D:].cpu(), qkv[:, (hq + hk) * D:]), "v part must be untouched"

@@ -16,6 +16,7 @@
 // ragged end of K) evaluate the per-element mask. Workgroups are ordered longest-first and grouped by
 // head inside each XCD (blockIdx round-robins over the 8 XCDs) so the K/V of a head stay in one L2.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 
@@ -56,6 +57,17 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
 }
 __device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// gfx950 transposing LDS read (ds_read_b64_tr_b16). Within each group of 16 lanes, lane m supplies the address
+// of 4 consecutive 16-bit elements M[m][0..3]; lane j receives M[4e + j/4][j%4] for e = 0..3.
+__device__ __forceinline__ bf16x4 tr_read(const __bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((bf16x4 __attribute__((address_space(3)))*)(p));
+}
+typedef __fp16 fp16x4_builtin __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f16x4 tr_read(const _Float16* p) {
+  return __builtin_bit_cast(
+      f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((fp16x4_builtin __attribute__((address_space(3)))*)(p)));
 }
 
 template <typename T>
@@ -116,12 +128,11 @@ __device__ __forceinline__ void map_block(int n_tiles, int bh_count, bool revers
 // Forward kernel.
 // ------------------------------------------------------------------------------------------------
 template <typename T, int D, int BN, bool MASK, bool SOFTCAP, bool REFROUND>
-__global__ void __launch_bounds__(kThreads) attn_fwd_kernel(AttnParams p) {
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2, 2))) attn_fwd_kernel(AttnParams p) {
   typedef typename T::scalar S;
   typedef typename T::vec8 V8;
   typedef typename T::vec4 V4;
-  constexpr int KP = D + 8;   // padded K row (elements)
-  constexpr int VP = BN + 4;  // padded V^T row (elements)
+  constexpr int KP = D + 8;   // padded K / V row (elements)
   constexpr int NKK = D / 16;      // MFMA k-steps over the head dim
   constexpr int NMB = BN / 32;     // 32-key blocks per tile
   constexpr int NDB = D / 32;      // 32-wide head-dim blocks of O^T
@@ -131,7 +142,7 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(AttnParams p) {
   static_assert(CHUNKS % kThreads == 0, "tile must split evenly over the workgroup");
 
   __shared__ __attribute__((aligned(16))) S Ks[2][BN][KP];
-  __shared__ __attribute__((aligned(16))) S Vt[2][D][VP];
+  __shared__ __attribute__((aligned(16))) S Vs[2][BN][KP];
 
   int qt, bh;
   map_block(p.n_tiles, p.B * p.Hq, true, qt, bh);
@@ -140,6 +151,8 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(AttnParams p) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, r = lane & 31, g = lane >> 5;
   const int q0 = qt * kBM;
   const int qi = q0 + 32 * w + r;  // this lane's query row
+  const int tr_krow = (lane & 15) >> 2;                              // key row within a group of 4
+  const int tr_dcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);     // head-dim column within a 32-wide block
 
   const S* qp = static_cast<const S*>(p.q) + b * p.q_sb + h * p.q_sh;
   const S* kp = static_cast<const S*>(p.k) + b * p.k_sb + hk * p.k_sh;
@@ -152,6 +165,10 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(AttnParams p) {
     if (qi < p.Sq) qf[kk] = ld16<V8>(qp + (int64_t)qi * p.q_ss + 16 * kk + 8 * g);
     else qf[kk] = V8{};
   }
+  // Re-define the Q registers here (after their loads complete) so that the main loop's wait counting does not
+  // treat them as results of outstanding vector-memory loads.
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk) asm volatile("" : "+v"(qf[kk]));
 
   // Key range of this query tile.
   const int q_last = min(q0 + kBM, p.Sq) - 1;
@@ -165,55 +182,68 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(AttnParams p) {
 #pragma unroll
   for (int i = 0; i < NDB; ++i) oacc[i] = f32x16{};
   float m_run = -INFINITY;  // reference maximum (value units)
-  float l_run = 0.f;        // partial row sum (this lane's half of the keys)
   const float c = score_coeff<SOFTCAP, REFROUND>(p);
 
+  // Global -> register staging of one K/V tile: each thread owns CPT adjacent 16-byte chunks of one key row of
+  // K and of V (coalesced rows; both stay row-major in LDS). Full tiles are addressed through two per-lane
+  // pointers that advance by one tile right before each load (so a pointer register is never rewritten while
+  // loads through it are in flight), the chunk index going into the immediate offset.
   V8 kreg[CPT], vreg[CPT];
-  auto load_tile = [&](int t) {
-    const int kb = t * BN;
+  constexpr int TPR = (D / 8) / CPT;        // threads per row
+  static_assert(TPR * CPT == D / 8 && kThreads / TPR == BN, "tile mapping");
+  const int k_row0 = tid / TPR, k_c0 = (tid % TPR) * CPT;
+  const int64_t k_step = (int64_t)BN * p.k_ss * (int64_t)sizeof(S), v_step = (int64_t)BN * p.v_ss * (int64_t)sizeof(S);
+  // pointers of tile t_begin - 1 (advanced before use)
+  gptr k_addr = to_gptr(kp + (int64_t)(k_row0 - BN) * p.k_ss + k_c0 * 8) + (int64_t)t_begin * k_step;
+  gptr v_addr = to_gptr(vp + (int64_t)(k_row0 - BN) * p.v_ss + k_c0 * 8) + (int64_t)t_begin * v_step;
+  auto load_full = [&]() {
+    k_addr += k_step;
+    v_addr += v_step;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int ch = tid + i * kThreads;
-      {  // K: lanes run along the head dim (coalesced rows)
-        const int key = ch / (D / 8), dc = ch % (D / 8);
-        const int kg = kb + key;
-        kreg[i] = kg < p.Sk ? ld16<V8>(kp + (int64_t)kg * p.k_ss + dc * 8) : V8{};
-      }
-      {  // V: lanes run along keys so the transposed LDS writes are conflict-free
-        const int key = ch % BN, dc = ch / BN;
-        const int kg = kb + key;
-        vreg[i] = kg < p.Sk ? ld16<V8>(vp + (int64_t)kg * p.v_ss + dc * 8) : V8{};
-      }
+      kreg[i] = ldg16<V8>(k_addr + 16 * i);
+      vreg[i] = ldg16<V8>(v_addr + 16 * i);
     }
   };
+  // Ragged last tile: rows past the end are clamped to the last row (masked, finite: contributes exactly 0).
+  auto load_ragged = [&](int t) {
+    k_addr += k_step;
+    v_addr += v_step;
+    const int kb = t * BN;
+    const int kr = min(k_row0, p.Sk - 1 - kb);  // >= 0 for every loaded tile
+    const S* kt = kp + (int64_t)(kb + kr) * p.k_ss + k_c0 * 8;
+    const S* vt = vp + (int64_t)(kb + kr) * p.v_ss + k_c0 * 8;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      kreg[i] = ld16<V8>(kt + i * 8);
+      vreg[i] = ld16<V8>(vt + i * 8);
+    }
+  };
+  auto tile_full = [&](int t) { return (t + 1) * BN <= p.Sk; };
   auto store_tile = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int ch = tid + i * kThreads;
-      {
-        const int key = ch / (D / 8), dc = ch % (D / 8);
-        *reinterpret_cast<V8*>(&Ks[buf][key][dc * 8]) = kreg[i];
-      }
-      {
-        const int key = ch % BN, dc = ch / BN;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) Vt[buf][dc * 8 + e][key] = vreg[i][e];
-      }
+      *reinterpret_cast<V8*>(&Ks[buf][k_row0][(k_c0 + i) * 8]) = kreg[i];
+      *reinterpret_cast<V8*>(&Vs[buf][k_row0][(k_c0 + i) * 8]) = vreg[i];
     }
   };
 
   if (t_begin < t_end) {
-    load_tile(t_begin);
+    if (tile_full(t_begin)) load_full();
+    else load_ragged(t_begin);
     store_tile(0);
   }
   __syncthreads();
 
-  for (int t = t_begin; t < t_end; ++t) {
-    const int buf = (t - t_begin) & 1;
-    const bool has_next = t + 1 < t_end;
-    if (has_next) load_tile(t + 1);
+  // Visible keys of this lane's query: lo <= key <= hi (bottom-right causal, sliding window, ragged end).
+  int k_hi = p.Sk - 1, k_lo = 0;
+  if (p.causal) k_hi = min(k_hi, qi + p.offset);
+  if (p.window > 0) k_lo = max(k_lo, qi + p.offset - p.window + 1);
+  float l_part[4] = {0.f, 0.f, 0.f, 0.f};  // split row sums (breaks the dependent add chain)
 
-    // S^T = K . Q^T
+  // One K/V tile: S^T = K.Q^T, scores, online softmax, O^T += V^T.P^T. MASKED tiles compare each key against
+  // the lane's [k_lo, k_hi]; all other tiles run without any mask arithmetic.
+  auto tile = [&](const int t, const int buf, auto masked) {
     f32x16 sacc[NMB];
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb) sacc[mb] = f32x16{};
@@ -225,29 +255,17 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(AttnParams p) {
         sacc[mb] = mfma32(a, qf[kk], sacc[mb]);
       }
     }
-
-    // Scores -> values, mask, row max.
-    const int kb = t * BN;
-    bool need_mask = kb + BN > p.Sk;
-    if constexpr (MASK) {
-      if (p.causal && kb + BN - 1 > q0 + p.offset) need_mask = true;
-      if (p.window > 0 && kb < q_last + p.offset - p.window + 1) need_mask = true;
-    }
+    // element (mb, j) holds key t*BN + mb*32 + 8*(j/4) + 4g + j%4
+    const int rel_hi = k_hi - (t * BN + 4 * g), rel_lo = k_lo - (t * BN + 4 * g);
     float mloc = -INFINITY;
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         float x = score_value<T, SOFTCAP, REFROUND>(sacc[mb][j], p);
-        if (need_mask) {
-          const int kj = kb + mb * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
-          bool ok = kj < p.Sk;
-          if constexpr (MASK) {
-            const int rel = qi + p.offset - kj;  // query position minus key position
-            if (p.causal) ok = ok && rel >= 0;
-            if (p.window > 0) ok = ok && rel < p.window;
-          }
-          x = ok ? x : -INFINITY;
+        if constexpr (decltype(masked)::value) {
+          const int o = mb * 32 + 8 * (j >> 2) + (j & 3);
+          x = (o <= rel_hi && o >= rel_lo) ? x : -INFINITY;
         }
         sacc[mb][j] = x;
         mloc = fmaxf(mloc, x);
@@ -259,35 +277,72 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(AttnParams p) {
     if (__any(need)) {
       const float alpha = need ? fast_exp2((m_run - m_new) * c) : 1.0f;
       if (need) m_run = m_new;
-      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) l_part[i] *= alpha;
 #pragma unroll
       for (int i = 0; i < NDB; ++i) oacc[i] *= alpha;
     }
     const float mc = m_run == -INFINITY ? 0.f : m_run * c;
 
-    // P = exp2(v*c - m*c), row-sum, pack to 16-bit B operands, O^T += V^T . P^T
+    // P = exp2(v*c - m*c), row sums, pack to 16-bit B operands, O^T += V^T . P^T
 #pragma unroll
     for (int kk = 0; kk < NPK; ++kk) {
       f32x8 pv;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float pe = fast_exp2(fmaf(sacc[kk >> 1][8 * (kk & 1) + e], c, -mc));
-        l_run += pe;
+        l_part[e & 3] += pe;
         pv[e] = pe;
       }
       const V8 pb = from_f32x8<V8>(pv);
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        const V4 lo = *reinterpret_cast<const V4*>(&Vt[buf][db * 32 + r][16 * kk + 4 * g]);
-        const V4 hi = *reinterpret_cast<const V4*>(&Vt[buf][db * 32 + r][16 * kk + 8 + 4 * g]);
+        // A = V^T rows db*32 + r, keys 16kk + 4g + {0..3} and 16kk + 8 + 4g + {0..3} (the P operand's key order),
+        // gathered from row-major V by the transposing read (lane m of each 16-lane group points at key row
+        // m/4 and head-dim column 4*(m%4) of its 16-column slab).
+        const S* vrow = &Vs[buf][16 * kk + 4 * g + tr_krow][db * 32 + tr_dcol];
+        const V4 lo = tr_read(vrow);
+        const V4 hi = tr_read(vrow + 8 * KP);
         const V8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         oacc[db] = mfma32(a, pb, oacc[db]);
       }
     }
+  };
 
-    if (has_next) store_tile(buf ^ 1);
-    __syncthreads();
+  // Tiles [t_begin, t_full0) and [t_full1, t_end) straddle the window's lower edge or the causal diagonal (or the
+  // ragged end of K) and evaluate the mask; tiles in between are visible to every row of the workgroup.
+  int t_full0 = t_begin, t_full1 = t_end;
+  if constexpr (MASK) {
+    if (p.window > 0) {  // first tile whose first key is visible to the last row
+      const int lo_last = q_last + p.offset - p.window + 1;
+      t_full0 = lo_last <= 0 ? t_begin : min(t_end, max(t_begin, (lo_last + BN - 1) / BN));
+    }
+    if (p.causal) {  // first tile whose last key is hidden from the first row
+      const int hi_first = q0 + p.offset;  // last key visible to the first row
+      t_full1 = max(t_full0, min(t_end, hi_first < 0 ? t_begin : (hi_first + 1) / BN));
+    }
   }
+  if (t_full1 > t_full0 && t_full1 * BN > p.Sk) t_full1 = max(t_full0, p.Sk / BN);
+  if (t_full1 < t_full0) t_full1 = t_full0;
+
+  // Full next tiles are prefetched into registers before this tile's compute; the ragged last tile (at most one)
+  // is loaded after it.
+  auto step = [&](const int t, auto masked) {
+    const int buf = (t - t_begin) & 1;
+    const int tn = t + 1;
+    const bool prefetch = tn < t_end && tile_full(tn);
+    if (prefetch) load_full();
+    tile(t, buf, masked);
+    if (tn < t_end) {
+      if (!prefetch) load_ragged(tn);
+      store_tile(buf ^ 1);
+    }
+    __syncthreads();
+  };
+  for (int t = t_begin; t < t_full0; ++t) step(t, std::true_type{});
+  for (int t = t_full0; t < t_full1; ++t) step(t, std::false_type{});
+  for (int t = t_full1; t < t_end; ++t) step(t, std::true_type{});
+  float l_run = (l_part[0] + l_part[1]) + (l_part[2] + l_part[3]);
 
   // Epilogue: full row sum, normalise, store O (4 consecutive head-dim elements per store) and lse.
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
@@ -350,6 +405,8 @@ __global__ void __launch_bounds__(kThreads) attn_colsum_kernel(AttnParams p) {
     if (kj < p.Sk) kf[kk] = ld16<V8>(kp + (int64_t)kj * p.k_ss + 16 * kk + 8 * g);
     else kf[kk] = V8{};
   }
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk) asm volatile("" : "+v"(kf[kk]));  // see the forward kernel
 
   // Query range that can see any key of this tile.
   const int k_last = min(k0 + kCBK, p.Sk) - 1;
@@ -513,9 +570,13 @@ int validate_attn(const char* op, const void* q, const void* k, int64_t B, int64
               "%s: size too large", op);
   DGG_REQUIRE(B * Hq * ((std::max(Sq, Sk) + 127) / 128) < (1ll << 31), DGG_ERR_SHAPE, "%s: grid too large", op);
   DGG_REQUIRE(strides != nullptr, DGG_ERR_NULL, "%s: strides is NULL", op);
-  for (int i = 0; i < nstrides; ++i)
+  for (int i = 0; i < nstrides; ++i) {
     DGG_REQUIRE(strides[i] >= 0 && strides[i] % 8 == 0, DGG_ERR_STRIDE,
                 "%s: stride[%d] = %lld must be a non-negative multiple of 8 elements", op, i, (long long)strides[i]);
+    // in-tile row offsets are 32-bit: 256 rows of the sequence stride must stay below 2^31 elements
+    DGG_REQUIRE(i % 3 != 1 || strides[i] < (1ll << 23), DGG_ERR_STRIDE,
+                "%s: sequence stride[%d] = %lld must be < 2^23 elements", op, i, (long long)strides[i]);
+  }
   DGG_REQUIRE(std::isfinite(scale) && scale > 0.f, DGG_ERR_SHAPE, "%s: scale must be finite and > 0", op);
   DGG_REQUIRE(softcap >= 0.f && std::isfinite(softcap), DGG_ERR_SHAPE, "%s: softcap must be >= 0 (0 = off)", op);
   DGG_REQUIRE(window >= 0 && window < (1ll << 30), DGG_ERR_SHAPE, "%s: window must be >= 0 (0 = off)", op);

@@ -87,6 +87,14 @@ __device__ __forceinline__ void st16(void* p, V v) {
   *reinterpret_cast<V*>(p) = v;
 }
 
+// Pointers in the global address space (loads through them are global_load_*, never flat_load_*).
+typedef const char __attribute__((address_space(1)))* gptr;
+template <typename V>
+__device__ __forceinline__ V ldg16(gptr p) {
+  return *reinterpret_cast<const V __attribute__((address_space(1)))*>(p);
+}
+__device__ __forceinline__ gptr to_gptr(const void* p) { return (gptr)(reinterpret_cast<uintptr_t>(p)); }
+
 // Wave64 reductions.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -6,12 +6,14 @@ fails to load, every op raises RuntimeError naming the path and how to build it.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent / "libdgg_hip.so"
+# DGG_LIBRARY overrides the in-tree library path (e.g. to compare builds).
+LIB_PATH = Path(os.environ.get("DGG_LIBRARY", Path(__file__).resolve().parent / "libdgg_hip.so"))
 
 DGG_F32, DGG_F16, DGG_BF16 = 0, 1, 2
 ATTN_CAUSAL = 0x1

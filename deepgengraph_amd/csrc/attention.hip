@@ -26,6 +26,12 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBM = 32 * kWaves;  // query rows per forward workgroup
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
+#ifndef DGG_KPAD
+#define DGG_KPAD 8
+#endif
+#ifndef DGG_VPAD
+#define DGG_VPAD 8
+#endif
 
 struct AttnParams {
   const void* q;
@@ -132,7 +138,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D
   typedef typename T::scalar S;
   typedef typename T::vec8 V8;
   typedef typename T::vec4 V4;
-  constexpr int KP = D + 8;   // padded K / V row (elements)
+  constexpr int KP = D + DGG_KPAD;   // padded K row (elements)
+  constexpr int VP = D + DGG_VPAD;   // padded V row (elements)
   constexpr int NKK = D / 16;      // MFMA k-steps over the head dim
   constexpr int NMB = BN / 32;     // 32-key blocks per tile
   constexpr int NDB = D / 32;      // 32-wide head-dim blocks of O^T
@@ -142,7 +149,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D
   static_assert(CHUNKS % kThreads == 0, "tile must split evenly over the workgroup");
 
   __shared__ __attribute__((aligned(16))) S Ks[2][BN][KP];
-  __shared__ __attribute__((aligned(16))) S Vs[2][BN][KP];
+  __shared__ __attribute__((aligned(16))) S Vs[2][BN][VP];
 
   int qt, bh;
   map_block(p.n_tiles, p.B * p.Hq, true, qt, bh);
@@ -302,7 +309,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D
         // m/4 and head-dim column 4*(m%4) of its 16-column slab).
         const S* vrow = &Vs[buf][16 * kk + 4 * g + tr_krow][db * 32 + tr_dcol];
         const V4 lo = tr_read(vrow);
-        const V4 hi = tr_read(vrow + 8 * KP);
+        const V4 hi = tr_read(vrow + 8 * VP);
         const V8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         oacc[db] = mfma32(a, pb, oacc[db]);
       }
@@ -362,6 +369,316 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D
     if (p.lse != nullptr && g == 0) {
       const float lse2 = m_run == -INFINITY ? -INFINITY : m_run * c + fast_log2(l_tot);
       p.lse[(int64_t)bh * p.Sq + qi] = lse2 * kLn2;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Forward kernel for head_dim 128: 4 waves x 64 query rows (two 32-row MFMA column blocks per wave, so every K
+// and V fragment read from LDS feeds two MFMAs), one wave per SIMD (accumulators may live in AGPRs). K/V tiles
+// of 64 keys are copied global -> LDS by the direct-to-LDS loads of gfx950 (no VGPR staging, no LDS store
+// instructions) into a 4-stage ring, so three tiles are in flight while one is computed, with one barrier per
+// tile. Each 16-byte chunk c of tile row r sits at
+//     (r/4)*GROUP_B + (r%4)*ROW_B + 16*(c ^ 4*(r%4))        (4-row groups padded by 16 bytes)
+// which keeps both the K fragment reads (16 lanes, 16 rows, one chunk) and the V transposing reads (4 rows x
+// 4 chunks per 16-lane group) on distinct LDS banks; the direct loads write that layout by fetching, for LDS
+// position p of a row, global chunk p ^ 4*(r%4).
+// ------------------------------------------------------------------------------------------------
+namespace d128 {
+constexpr int D = 128;
+constexpr int BN = 64;                     // keys per tile
+constexpr int NSTAGE = 4;
+constexpr int ROW_B = D * 2;               // bytes per K/V row
+constexpr int GROUP_B = 4 * ROW_B + 16;    // 4-row group + pad
+constexpr int TILE_B = (BN / 4) * GROUP_B;
+constexpr int STAGE_B = 2 * TILE_B;        // K tile, then V tile
+}  // namespace d128
+
+typedef __attribute__((address_space(3))) char lds_char;
+
+template <typename V>
+__device__ __forceinline__ V lds_read(uint32_t addr) {
+  return *reinterpret_cast<const V __attribute__((address_space(3)))*>((lds_char*)(size_t)addr);
+}
+__device__ __forceinline__ bf16x4 tr_read_at(uint32_t addr, __bf16) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((bf16x4 __attribute__((address_space(3)))*)(size_t)addr);
+}
+__device__ __forceinline__ f16x4 tr_read_at(uint32_t addr, _Float16) {
+  return __builtin_bit_cast(
+      f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((fp16x4_builtin __attribute__((address_space(3)))*)(size_t)addr));
+}
+
+// Direct global -> LDS copy (global_load_lds_dwordx4): lane l's 16 bytes land at LDS byte address lds + 16*l.
+// The copy is not tracked by the compiler's wait counting; callers wait with wait_vmem().
+__device__ __forceinline__ void dma16(uint32_t lds, const void* sbase, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(sbase)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma16(uint32_t lds, const void* vaddr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(vaddr)
+               : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// NQB: 32-row query blocks per wave (each K / V fragment feeds NQB MFMAs); NW: waves per workgroup.
+template <typename T, int NQB, int NW, bool MASK, bool SOFTCAP, bool REFROUND>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NQB * NW / 4 == 1 ? 1 : 2, 2)))
+attn_fwd_d128_kernel(AttnParams p) {
+  using namespace d128;
+  typedef typename T::scalar S;
+  typedef typename T::vec8 V8;
+  typedef typename T::vec4 V4;
+  constexpr int QPW = 32 * NQB;                 // query rows per wave
+  constexpr int BM = QPW * NW;                  // query rows per workgroup
+  constexpr int GPW = (BN / 4) / NW;            // 4-row groups of a tile copied by each wave (K and V each)
+  constexpr int DMA_PER_TILE = 2 * GPW;         // direct loads per wave per tile
+  static_assert(GPW >= 1 && GPW * NW == BN / 4, "tile groups must split over the waves");
+  __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * STAGE_B];
+
+  int qt, bh;
+  map_block(p.n_tiles, p.B * p.Hq, true, qt, bh);
+  const int b = bh / p.Hq, h = bh - b * p.Hq;
+  const int hk = h / p.group;
+  const int tid = threadIdx.x, lane = tid & 63, r = lane & 31, g = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q0 = qt * BM;
+  const int qw0 = q0 + QPW * w;  // first query row of this wave; lane rows qw0 + 32n + r, n = 0, 1
+
+  const S* qp = static_cast<const S*>(p.q) + b * p.q_sb + h * p.q_sh;
+  const char* kp = reinterpret_cast<const char*>(static_cast<const S*>(p.k) + b * p.k_sb + hk * p.k_sh);
+  const char* vp = reinterpret_cast<const char*>(static_cast<const S*>(p.v) + b * p.v_sb + hk * p.v_sh);
+  const int64_t k_ss_b = p.k_ss * (int64_t)sizeof(S), v_ss_b = p.v_ss * (int64_t)sizeof(S);
+
+  V8 qf[NQB][D / 16];
+#pragma unroll
+  for (int n = 0; n < NQB; ++n) {
+    const int qi = qw0 + 32 * n + r;
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+      if (qi < p.Sq) qf[n][kk] = ld16<V8>(qp + (int64_t)qi * p.q_ss + 16 * kk + 8 * g);
+      else qf[n][kk] = V8{};
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < NQB; ++n)
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(qf[n][kk]));
+
+  // Key tiles of the workgroup and of this wave.
+  const int q_last = min(q0 + BM, p.Sq) - 1;
+  int k_begin = 0, k_end = p.Sk;
+  if (p.causal) k_end = min(p.Sk, q_last + p.offset + 1);
+  if (p.window > 0) k_begin = max(0, q0 + p.offset - p.window + 1);
+  const int t_begin = k_begin / BN;
+  const int t_end = k_end > k_begin ? (k_end + BN - 1) / BN : t_begin;
+  const int wq_last = min(qw0 + QPW, p.Sq) - 1;  // may be < qw0 for a wave past the end
+  int wk_begin = 0, wk_end = p.Sk;
+  if (p.causal) wk_end = min(p.Sk, wq_last + p.offset + 1);
+  if (p.window > 0) wk_begin = max(0, qw0 + p.offset - p.window + 1);
+
+  // Visible keys per lane row: lo <= key <= hi.
+  int k_hi[NQB], k_lo[NQB];
+#pragma unroll
+  for (int n = 0; n < NQB; ++n) {
+    const int qi = qw0 + 32 * n + r;
+    k_hi[n] = p.Sk - 1;
+    k_lo[n] = 0;
+    if (p.causal) k_hi[n] = min(k_hi[n], qi + p.offset);
+    if (p.window > 0) k_lo[n] = max(k_lo[n], qi + p.offset - p.window + 1);
+  }
+
+  // Direct-load lane constants: lane l fills LDS position l%16 of row l/16 of a 4-row group, fetching global
+  // chunk (l%16) ^ 4*(l/16).
+  const int rr = lane >> 4;
+  const uint32_t src_chunk = (uint32_t)((lane & 15) ^ (rr << 2));
+  uint32_t k_voff = (uint32_t)(rr * k_ss_b) + src_chunk * 16u;
+  uint32_t v_voff = (uint32_t)(rr * v_ss_b) + src_chunk * 16u;
+  asm volatile("" : "+v"(k_voff), "+v"(v_voff));
+  const uint32_t smem_base = (uint32_t)(size_t)((lds_char*)smem);
+
+  // Copies groups GPW*w .. GPW*w + GPW-1 of tile t into stage t % NSTAGE: DMA_PER_TILE loads per wave.
+  auto issue = [&](int t) {
+    const uint32_t kdst = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B + GPW * w * GROUP_B);
+    const uint32_t vdst = kdst + TILE_B;
+    const int row0 = t * BN + 4 * GPW * w;
+    if ((t + 1) * BN <= p.Sk) {
+      const char* kb = kp + (int64_t)row0 * k_ss_b;
+      const char* vb = vp + (int64_t)row0 * v_ss_b;
+#pragma unroll
+      for (int j = 0; j < GPW; ++j) {
+        dma16(kdst + j * GROUP_B, kb + 4 * j * k_ss_b, k_voff);
+        dma16(vdst + j * GROUP_B, vb + 4 * j * v_ss_b, v_voff);
+      }
+    } else {  // ragged last tile: rows past the end re-read the last row (always masked, finite)
+#pragma unroll
+      for (int j = 0; j < GPW; ++j) {
+        const int64_t row = min(row0 + 4 * j + rr, p.Sk - 1);
+        dma16(kdst + j * GROUP_B, kp + row * k_ss_b + src_chunk * 16);
+        dma16(vdst + j * GROUP_B, vp + row * v_ss_b + src_chunk * 16);
+      }
+    }
+  };
+
+  // LDS read addressing. K fragment (row mb*32 + r, chunk 2kk + g): lane part + xk[kk/2] + constant.
+  // V transposing read (rows 16kk + 4g + (lane%16)/4 (+8), head-dim column db*32 + 16*((lane/16)%2) + 4*(lane%4)):
+  // lane part + xv[db] + constant.
+  const int s4 = r & 3;
+  const uint32_t k_lane = (uint32_t)((r >> 2) * GROUP_B + s4 * ROW_B + 16 * g);
+  uint32_t xk[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xk[i] = k_lane + 64u * (uint32_t)(i ^ s4);
+  const int m4 = (lane & 15) >> 2, m3 = lane & 3;
+  const uint32_t v_lane = (uint32_t)(TILE_B + g * GROUP_B + m4 * ROW_B + 32 * ((lane >> 4) & 1) + 16 * (m3 >> 1) +
+                                     8 * (m3 & 1));
+  uint32_t xv[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) xv[db] = v_lane + 64u * (uint32_t)(db ^ m4);
+
+  f32x16 oacc[NQB][D / 32];
+  float m_run[NQB], l_part[NQB][2];
+#pragma unroll
+  for (int n = 0; n < NQB; ++n) {
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) oacc[n][i] = f32x16{};
+    m_run[n] = -INFINITY;
+    l_part[n][0] = l_part[n][1] = 0.f;
+  }
+  const float c = score_coeff<SOFTCAP, REFROUND>(p);
+
+  auto tile = [&](const int t, auto masked) {
+    const uint32_t st = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B);
+    f32x16 sacc[NQB][2];
+#pragma unroll
+    for (int n = 0; n < NQB; ++n) sacc[n][0] = sacc[n][1] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const V8 a = lds_read<V8>(st + xk[kk >> 1] + mb * 8 * GROUP_B + 32 * (kk & 1));
+#pragma unroll
+        for (int n = 0; n < NQB; ++n) sacc[n][mb] = mfma32(a, qf[n][kk], sacc[n][mb]);
+      }
+    }
+    const int kb4 = t * BN + 4 * g;
+#pragma unroll
+    for (int n = 0; n < NQB; ++n) {
+      const int rel_hi = k_hi[n] - kb4, rel_lo = k_lo[n] - kb4;
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          float x = score_value<T, SOFTCAP, REFROUND>(sacc[n][mb][j], p);
+          if constexpr (decltype(masked)::value) {
+            const int o = mb * 32 + 8 * (j >> 2) + (j & 3);
+            x = (o <= rel_hi && o >= rel_lo) ? x : -INFINITY;
+          }
+          sacc[n][mb][j] = x;
+          mloc = fmaxf(mloc, x);
+        }
+      }
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      const float m_new = fmaxf(m_run[n], mloc);
+      const bool need = m_new * c > m_run[n] * c + kRescaleThreshold;
+      if (__any(need)) {
+        const float alpha = need ? fast_exp2((m_run[n] - m_new) * c) : 1.0f;
+        if (need) m_run[n] = m_new;
+        l_part[n][0] *= alpha;
+        l_part[n][1] *= alpha;
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i) oacc[n][i] *= alpha;
+      }
+    }
+    float mcs[NQB];
+#pragma unroll
+    for (int n = 0; n < NQB; ++n) mcs[n] = m_run[n] == -INFINITY ? 0.f : m_run[n] * c;
+#pragma unroll
+    for (int kk = 0; kk < BN / 16; ++kk) {
+      V8 pb[NQB];
+#pragma unroll
+      for (int n = 0; n < NQB; ++n) {
+        const float mc = mcs[n];
+        f32x8 pv;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pe = fast_exp2(fmaf(sacc[n][kk >> 1][8 * (kk & 1) + e], c, -mc));
+          l_part[n][e & 1] += pe;
+          pv[e] = pe;
+        }
+        pb[n] = from_f32x8<V8>(pv);
+      }
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) {
+        const V4 lo = tr_read_at(st + xv[db] + kk * 4 * GROUP_B, S{});
+        const V4 hi = tr_read_at(st + xv[db] + kk * 4 * GROUP_B + 2 * GROUP_B, S{});
+        const V8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+        for (int n = 0; n < NQB; ++n) oacc[n][db] = mfma32(a, pb[n], oacc[n][db]);
+      }
+    }
+  };
+
+  // Tile classes, as in the generic kernel but per wave: tiles outside [wk_begin, wk_end) are skipped by this
+  // wave (it still takes part in the loads and barriers); [t_full0, t_full1) needs no mask for any of its rows.
+  int t_full0 = t_begin, t_full1 = t_end;
+  if constexpr (MASK) {
+    if (p.window > 0) {
+      const int lo_last = wq_last + p.offset - p.window + 1;
+      t_full0 = lo_last <= 0 ? t_begin : min(t_end, max(t_begin, (lo_last + BN - 1) / BN));
+    }
+    if (p.causal) {
+      const int hi_first = qw0 + p.offset;
+      t_full1 = max(t_full0, min(t_end, hi_first < 0 ? t_begin : (hi_first + 1) / BN));
+    }
+  }
+  if (t_full1 > t_full0 && t_full1 * BN > p.Sk) t_full1 = max(t_full0, p.Sk / BN);
+  if (t_full1 < t_full0) t_full1 = t_full0;
+  const int wt_begin = wk_begin / BN;
+  const int wt_end = wk_end > wk_begin ? (wk_end + BN - 1) / BN : wt_begin;
+
+  // Pipeline: tiles t+1 .. t+NSTAGE-2 may still be in flight while tile t is waited for; the copy of tile
+  // t+NSTAGE-1 is issued after the barrier into the stage that held tile t-1.
+#pragma unroll
+  for (int i = 0; i < NSTAGE - 1; ++i)
+    if (t_begin + i < t_end) issue(t_begin + i);
+  auto step = [&](const int t, auto masked) {
+    const int after = min(NSTAGE - 2, t_end - 1 - t);
+    if (after >= 2) wait_vmem<2 * DMA_PER_TILE>();
+    else if (after == 1) wait_vmem<DMA_PER_TILE>();
+    else wait_vmem<0>();
+    __syncthreads();
+    if (t + NSTAGE - 1 < t_end) issue(t + NSTAGE - 1);
+    if (t >= wt_begin && t < wt_end) tile(t, masked);
+  };
+  for (int t = t_begin; t < t_full0; ++t) step(t, std::true_type{});
+  for (int t = t_full0; t < t_full1; ++t) step(t, std::false_type{});
+  for (int t = t_full1; t < t_end; ++t) step(t, std::true_type{});
+
+#pragma unroll
+  for (int n = 0; n < NQB; ++n) {
+    const int qi = qw0 + 32 * n + r;
+    const float l_run = l_part[n][0] + l_part[n][1];
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float inv = 1.0f / l_tot;
+    if (qi < p.Sq) {
+      S* op = static_cast<S*>(p.o) + b * p.o_sb + (int64_t)qi * p.o_ss + h * p.o_sh;
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          V4 ov;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ov[e] = to_s<S>(oacc[n][db][4 * jj + e] * inv);
+          *reinterpret_cast<V4*>(op + db * 32 + 8 * jj + 4 * g) = ov;
+        }
+      }
+      if (p.lse != nullptr && g == 0) {
+        const float lse2 = m_run[n] == -INFINITY ? -INFINITY : m_run[n] * c + fast_log2(l_tot);
+        p.lse[(int64_t)bh * p.Sq + qi] = lse2 * kLn2;
+      }
     }
   }
 }
@@ -518,11 +835,32 @@ void launch_colsum(const AttnParams& p, hipStream_t st) {
   hipLaunchKernelGGL((attn_colsum_kernel<T, D, MASK, SOFTCAP, REFROUND>), dim3(grid), dim3(kThreads), 0, st, p);
 }
 
+#ifndef DGG_D128_NQB
+#define DGG_D128_NQB 1
+#endif
+#ifndef DGG_D128_NW
+#define DGG_D128_NW 8
+#endif
+constexpr int kD128NQB = DGG_D128_NQB, kD128NW = DGG_D128_NW;
+constexpr int kD128BM = 32 * kD128NQB * kD128NW;  // query rows per workgroup of the head_dim-128 kernel
+
+template <typename T, bool MASK, bool SOFTCAP, bool REFROUND>
+void launch_fwd_d128(const AttnParams& p, hipStream_t st) {
+  const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
+  hipLaunchKernelGGL((attn_fwd_d128_kernel<T, kD128NQB, kD128NW, MASK, SOFTCAP, REFROUND>), dim3(grid),
+                     dim3(64 * kD128NW), 0, st, p);
+}
+
 template <typename T, int D, bool MASK, bool SOFTCAP>
 void pick_fwd_ref(const AttnParams& p, bool ref, hipStream_t st) {
   constexpr int BN = D >= 256 ? 32 : 64;
-  if (ref) launch_fwd<T, D, BN, MASK, SOFTCAP, true>(p, st);
-  else launch_fwd<T, D, BN, MASK, SOFTCAP, false>(p, st);
+  if constexpr (D == 128) {
+    if (ref) launch_fwd_d128<T, MASK, SOFTCAP, true>(p, st);
+    else launch_fwd_d128<T, MASK, SOFTCAP, false>(p, st);
+  } else {
+    if (ref) launch_fwd<T, D, BN, MASK, SOFTCAP, true>(p, st);
+    else launch_fwd<T, D, BN, MASK, SOFTCAP, false>(p, st);
+  }
 }
 template <typename T, int D>
 void pick_fwd(const AttnParams& p, bool ref, hipStream_t st) {
@@ -628,7 +966,8 @@ extern "C" int dgg_attn_prefill(const void* q, const void* k, const void* v, voi
   p.k_sb = strides[3]; p.k_ss = strides[4]; p.k_sh = strides[5];
   p.v_sb = strides[6]; p.v_ss = strides[7]; p.v_sh = strides[8];
   p.o_sb = strides[9]; p.o_ss = strides[10]; p.o_sh = strides[11];
-  p.n_tiles = (int)((Sq + kBM - 1) / kBM);
+  const int64_t bm = D == 128 ? kD128BM : kBM;
+  p.n_tiles = (int)((Sq + bm - 1) / bm);
   const bool ref = (flags & DGG_ATTN_REF_ROUNDING) != 0;
   hipStream_t st = dgg::as_stream(stream);
   // Sk == 0 still launches: with no key tiles every row ends fully masked (o NaN, lse -inf), like any

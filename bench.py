@@ -154,6 +154,32 @@ def bench_block(args, dev):
     return dict(ms=round(ms, 4))
 
 
+def bench_copycal(args, dev):
+    """A plain device copy of known size (256 MiB read + 256 MiB written): the reference point that scales the
+    FETCH_SIZE / WRITE_SIZE counters of the profiled kernels to bytes."""
+    n = 256 * 1024 * 1024
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    ms = statistics.mean(_events_time(lambda: dst.copy_(src), 5, 1))
+    return dict(bytes_read=n, bytes_written=n, ms=round(ms, 4), gbps=round(2 * n / (ms * 1e-3) / 1e9, 1))
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary (profiles/traffic.json):
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the kernel, each divided by the same counter's reading for
+    the calibration copy and multiplied by the copy's known byte count. None if not measured."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        k, cal = t["kernels"][kernel], t["copy_calibration"]
+        rd = k["FETCH_SIZE_KiB"] / cal["FETCH_SIZE_KiB"] * cal["bytes_read"]
+        wr = k["WRITE_SIZE_KiB"] / cal["WRITE_SIZE_KiB"] * cal["bytes_written"]
+        return int(rd + wr)
+    except (OSError, KeyError, ValueError, ZeroDivisionError):
+        return None
+
+
 def cpu_baseline(target_s: float = 10.0):
     """Oracle (reference formula, PyTorch eager on the host CPU) on config 2's attention (all 32 heads, full
     sequence), repeated until ~target_s seconds of CPU work; the median run is reported."""
@@ -207,6 +233,8 @@ def main():
         extra["variants"] = bench_variants(args, dev)
     if "block" in sections:
         extra["cfg2_block_ms"] = bench_block(args, dev)["ms"]
+    if "copycal" in sections:
+        extra["copy_calibration"] = bench_copycal(args, dev)
     line = {
         "metric": METRIC,
         "value": round(pre["tflops_wall"], 2),
@@ -224,8 +252,8 @@ def main():
                    "D": cfg.D, "causal": True, "flop_model": "4*B*H*S^2*D/2 (run_kernel.py:24)",
                    "flops_per_step": pre["flops"], "exact_pair_flops": pre["exact_flops"]},
         "roofline": {"bound": "mfma", "achieved": round(pre["tflops_kern"], 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(pre["tflops_kern"] / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel_ms": round(pre["kern_ms"], 5)},
+                     "unit": "TFLOP/s", "frac": round(pre["tflops_kern"] / PEAK_BF16_TFLOPS, 4),
+                     "traffic": measured_traffic("attn_fwd_d128_kernel"), "kernel_ms": round(pre["kern_ms"], 5)},
     }
     line.update(extra)
     if not args.no_cpu_baseline:

@@ -26,12 +26,7 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBM = 32 * kWaves;  // query rows per forward workgroup
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
-#ifndef DGG_KPAD
-#define DGG_KPAD 8
-#endif
-#ifndef DGG_VPAD
-#define DGG_VPAD 8
-#endif
+
 
 struct AttnParams {
   const void* q;
@@ -138,8 +133,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D
   typedef typename T::scalar S;
   typedef typename T::vec8 V8;
   typedef typename T::vec4 V4;
-  constexpr int KP = D + DGG_KPAD;   // padded K row (elements)
-  constexpr int VP = D + DGG_VPAD;   // padded V row (elements)
+  constexpr int KP = D + 8;  // padded K row (elements): 16-byte shift per row for the fragment reads
+  constexpr int VP = D + 8;  // padded V row (elements): 16-byte shift per row for the transposing reads
   constexpr int NKK = D / 16;      // MFMA k-steps over the head dim
   constexpr int NMB = BN / 32;     // 32-key blocks per tile
   constexpr int NDB = D / 32;      // 32-wide head-dim blocks of O^T
@@ -386,12 +381,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D
 // ------------------------------------------------------------------------------------------------
 namespace d128 {
 constexpr int D = 128;
-constexpr int BN = 64;                     // keys per tile
-constexpr int NSTAGE = 4;
 constexpr int ROW_B = D * 2;               // bytes per K/V row
 constexpr int GROUP_B = 4 * ROW_B + 16;    // 4-row group + pad
-constexpr int TILE_B = (BN / 4) * GROUP_B;
-constexpr int STAGE_B = 2 * TILE_B;        // K tile, then V tile
 }  // namespace d128
 
 typedef __attribute__((address_space(3))) char lds_char;
@@ -423,8 +414,9 @@ __device__ __forceinline__ void wait_vmem() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// NQB: 32-row query blocks per wave (each K / V fragment feeds NQB MFMAs); NW: waves per workgroup.
-template <typename T, int NQB, int NW, bool MASK, bool SOFTCAP, bool REFROUND>
+// NQB: 32-row query blocks per wave (each K / V fragment feeds NQB MFMAs); NW: waves per workgroup; BN: keys
+// per tile; NSTAGE: tiles in the LDS ring.
+template <typename T, int NQB, int NW, int BN, int NSTAGE, bool MASK, bool SOFTCAP, bool REFROUND>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NQB * NW / 4 == 1 ? 1 : 2, 2)))
 attn_fwd_d128_kernel(AttnParams p) {
   using namespace d128;
@@ -433,6 +425,8 @@ attn_fwd_d128_kernel(AttnParams p) {
   typedef typename T::vec4 V4;
   constexpr int QPW = 32 * NQB;                 // query rows per wave
   constexpr int BM = QPW * NW;                  // query rows per workgroup
+  constexpr int TILE_B = (BN / 4) * GROUP_B;
+  constexpr int STAGE_B = 2 * TILE_B;           // K tile, then V tile
   constexpr int GPW = (BN / 4) / NW;            // 4-row groups of a tile copied by each wave (K and V each)
   constexpr int DMA_PER_TILE = 2 * GPW;         // direct loads per wave per tile
   static_assert(GPW >= 1 && GPW * NW == BN / 4, "tile groups must split over the waves");
@@ -550,13 +544,16 @@ attn_fwd_d128_kernel(AttnParams p) {
 
   auto tile = [&](const int t, auto masked) {
     const uint32_t st = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B);
-    f32x16 sacc[NQB][2];
+    constexpr int NMB = BN / 32;
+    f32x16 sacc[NQB][NMB];
 #pragma unroll
-    for (int n = 0; n < NQB; ++n) sacc[n][0] = sacc[n][1] = f32x16{};
+    for (int n = 0; n < NQB; ++n)
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb) sacc[n][mb] = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
+      for (int mb = 0; mb < NMB; ++mb) {
         const V8 a = lds_read<V8>(st + xk[kk >> 1] + mb * 8 * GROUP_B + 32 * (kk & 1));
 #pragma unroll
         for (int n = 0; n < NQB; ++n) sacc[n][mb] = mfma32(a, qf[n][kk], sacc[n][mb]);
@@ -568,7 +565,7 @@ attn_fwd_d128_kernel(AttnParams p) {
       const int rel_hi = k_hi[n] - kb4, rel_lo = k_lo[n] - kb4;
       float mloc = -INFINITY;
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
+      for (int mb = 0; mb < NMB; ++mb) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           float x = score_value<T, SOFTCAP, REFROUND>(sacc[n][mb][j], p);
@@ -646,8 +643,8 @@ attn_fwd_d128_kernel(AttnParams p) {
     if (t_begin + i < t_end) issue(t_begin + i);
   auto step = [&](const int t, auto masked) {
     const int after = min(NSTAGE - 2, t_end - 1 - t);
-    if (after >= 2) wait_vmem<2 * DMA_PER_TILE>();
-    else if (after == 1) wait_vmem<DMA_PER_TILE>();
+    if (NSTAGE >= 4 && after >= 2) wait_vmem<2 * DMA_PER_TILE>();
+    else if (NSTAGE >= 3 && after >= 1) wait_vmem<DMA_PER_TILE>();
     else wait_vmem<0>();
     __syncthreads();
     if (t + NSTAGE - 1 < t_end) issue(t + NSTAGE - 1);
@@ -835,19 +832,14 @@ void launch_colsum(const AttnParams& p, hipStream_t st) {
   hipLaunchKernelGGL((attn_colsum_kernel<T, D, MASK, SOFTCAP, REFROUND>), dim3(grid), dim3(kThreads), 0, st, p);
 }
 
-#ifndef DGG_D128_NQB
-#define DGG_D128_NQB 1
-#endif
-#ifndef DGG_D128_NW
-#define DGG_D128_NW 8
-#endif
-constexpr int kD128NQB = DGG_D128_NQB, kD128NW = DGG_D128_NW;
-constexpr int kD128BM = 32 * kD128NQB * kD128NW;  // query rows per workgroup of the head_dim-128 kernel
+// head_dim 128 configuration (measured on MI355X, config 2): 8 waves x 32 rows, 128-key tiles, 2-stage ring.
+constexpr int kD128NQB = 1, kD128NW = 8, kD128BN = 128, kD128NS = 2;
+constexpr int kD128BM = 32 * kD128NQB * kD128NW;  // query rows per workgroup (head_dim 128)
 
 template <typename T, bool MASK, bool SOFTCAP, bool REFROUND>
 void launch_fwd_d128(const AttnParams& p, hipStream_t st) {
   const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
-  hipLaunchKernelGGL((attn_fwd_d128_kernel<T, kD128NQB, kD128NW, MASK, SOFTCAP, REFROUND>), dim3(grid),
+  hipLaunchKernelGGL((attn_fwd_d128_kernel<T, kD128NQB, kD128NW, kD128BN, kD128NS, MASK, SOFTCAP, REFROUND>), dim3(grid),
                      dim3(64 * kD128NW), 0, st, p);
 }
 

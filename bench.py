@@ -208,8 +208,8 @@ def cpu_baseline(target_s: float = 10.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sections", default="prefill,decode,prestep,variants,block")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()

@@ -46,6 +46,8 @@ struct AttnParams {
   int offset;    // Sk - Sq (bottom-right aligned causal mask)
   float scale;
   float ref_div;  // 1 / scale rounded to fp32 (== fp32 sqrt(D) for the usual scale): the reference divides
+                  // the rounded scores by it
+  float ref_rcp;  // 1 / ref_div rounded to fp32
   float c_fast;  // scale * log2(e): converts raw scores to the exp2 domain
   float inv_softcap;
   float softcap;
@@ -76,6 +78,21 @@ __device__ __forceinline__ float round_t(float x) {
   return to_f<typename T::scalar>(to_s<typename T::scalar>(x));
 }
 
+// x / d for the reference-rounding mode, from y = RN(1/d): q = RN(x*y), r = x - q*d (exact in one fma),
+// q' = RN(q + r*y). By Markstein's theorem (y within half an ulp of 1/d, q within one ulp of x/d) q' is the
+// correctly rounded quotient RN(x/d) whenever no intermediate underflows or overflows. Every caller rounds
+// q' on to fp16 / bf16 at once; checked exhaustively over all 2^16 fp16 and bf16 x for the usual divisors
+// and 200 random ones in [0.01, 1000] (tests/test_ref_division.py), the rounded results equal those of the
+// true division (up to the sign of a zero quotient, which no later step sees). The clamp keeps x = +-inf (a
+// score that overflowed fp16) from turning into inf - inf: it yields +-inf like the division does. Three
+// fma-class instructions and a clamp instead of the ~10 of the IEEE division sequence.
+__device__ __forceinline__ float ref_quot(float x, float d, float y) {
+  float q = fmaf(x, y, 0.0f);  // +0 addend keeps v_fma_mix (a -0 addend folds to a plain multiply)
+  q = __builtin_amdgcn_fmed3f(q, -3.402823466e38f, 3.402823466e38f);
+  const float r = fmaf(-q, d, x);
+  return fmaf(r, y, q);
+}
+
 // Score transform shared by the forward and column-sum kernels. Returns the value whose exp2 (after the
 // row maximum / lse is subtracted and `c` applied) is the unnormalised probability:
 //   fast path (no soft-cap, no reference rounding): the raw fp32 score; the caller multiplies by c_fast.
@@ -86,9 +103,9 @@ __device__ __forceinline__ float score_value(float s, const AttnParams& p) {
     // deepgengraph_exp/cases/kernels/attn.py:29 / gemma2.py:29-33: each step rounded to the input dtype;
     // `/ math.sqrt(D)` is an fp32 true division before the rounding.
     s = round_t<T>(s);
-    s = round_t<T>(s / p.ref_div);
+    s = round_t<T>(ref_quot(s, p.ref_div, p.ref_rcp));
     if constexpr (SOFTCAP) {
-      s = round_t<T>(s / p.softcap);
+      s = round_t<T>(ref_quot(s, p.softcap, p.inv_softcap));
       s = round_t<T>(tanhf(s));
       s = round_t<T>(s * p.softcap);
     }
@@ -105,6 +122,16 @@ __device__ __forceinline__ float score_value(float s, const AttnParams& p) {
 template <bool SOFTCAP, bool REFROUND>
 __device__ __forceinline__ float score_coeff(const AttnParams& p) {
   return (SOFTCAP || REFROUND) ? 1.0f : p.c_fast;
+}
+
+// Reference-rounded fp16 scores of two raw fp32 dot products, kept packed (natural-log domain): the matmul
+// output rounded to fp16, divided by ref_div, rounded again (attn.py:29 / h2o.py:29). The conversions are
+// v_cvt_pk_f16_f32 and the fp16 operands feed v_fma_mix_f32 directly, so the pair costs ten instructions.
+__device__ __forceinline__ f16x2 ref_scores_f16(float a, float b, const AttnParams& p) {
+  const f16x2 h = __builtin_convertvector(f32x2{a, b}, f16x2);
+  const float q0 = ref_quot((float)h[0], p.ref_div, p.ref_rcp);
+  const float q1 = ref_quot((float)h[1], p.ref_div, p.ref_rcp);
+  return __builtin_convertvector(f32x2{q0, q1}, f16x2);
 }
 
 // Maps blockIdx.x to (tile, batch*head). Longest tiles first; when the (batch, head) count divides by 8,
@@ -540,7 +567,9 @@ attn_fwd_d128_kernel(AttnParams p) {
     m_run[n] = -INFINITY;
     l_part[n][0] = l_part[n][1] = 0.f;
   }
-  const float c = score_coeff<SOFTCAP, REFROUND>(p);
+  // fp16 reference rounding without soft-cap keeps the scores as packed fp16 in the natural-log domain.
+  constexpr bool PK = REFROUND && !SOFTCAP && std::is_same<T, F16>::value;
+  const float c = PK ? kLog2e : score_coeff<SOFTCAP, REFROUND>(p);
 
   auto tile = [&](const int t, auto masked) {
     const uint32_t st = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B);
@@ -560,21 +589,40 @@ attn_fwd_d128_kernel(AttnParams p) {
       }
     }
     const int kb4 = t * BN + 4 * g;
+    constexpr bool PKM = PK && !decltype(masked)::value;  // scores stay packed fp16 through the P stage
+    f16x2 hs[NQB][NMB][8];
 #pragma unroll
     for (int n = 0; n < NQB; ++n) {
       const int rel_hi = k_hi[n] - kb4, rel_lo = k_lo[n] - kb4;
       float mloc = -INFINITY;
+      if constexpr (PK) {
 #pragma unroll
-      for (int mb = 0; mb < NMB; ++mb) {
+        for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          float x = score_value<T, SOFTCAP, REFROUND>(sacc[n][mb][j], p);
-          if constexpr (decltype(masked)::value) {
-            const int o = mb * 32 + 8 * (j >> 2) + (j & 3);
-            x = (o <= rel_hi && o >= rel_lo) ? x : -INFINITY;
+          for (int jp = 0; jp < 8; ++jp) hs[n][mb][jp] = ref_scores_f16(sacc[n][mb][2 * jp], sacc[n][mb][2 * jp + 1], p);
+      }
+      if constexpr (PKM) {
+        f16x2 mx = hs[n][0][0];
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+          for (int jp = 0; jp < 8; ++jp) mx = __builtin_elementwise_max(mx, hs[n][mb][jp]);
+        mloc = fmaxf((float)mx[0], (float)mx[1]);
+      } else {
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            float x;
+            if constexpr (PK) x = (float)hs[n][mb][j >> 1][j & 1];
+            else x = score_value<T, SOFTCAP, REFROUND>(sacc[n][mb][j], p);
+            if constexpr (decltype(masked)::value) {
+              const int o = mb * 32 + 8 * (j >> 2) + (j & 3);
+              x = (o <= rel_hi && o >= rel_lo) ? x : -INFINITY;
+            }
+            sacc[n][mb][j] = x;
+            mloc = fmaxf(mloc, x);
           }
-          sacc[n][mb][j] = x;
-          mloc = fmaxf(mloc, x);
         }
       }
       mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
@@ -601,7 +649,10 @@ attn_fwd_d128_kernel(AttnParams p) {
         f32x8 pv;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float pe = fast_exp2(fmaf(sacc[n][kk >> 1][8 * (kk & 1) + e], c, -mc));
+          float x;
+          if constexpr (PKM) x = (float)hs[n][kk >> 1][4 * (kk & 1) + (e >> 1)][e & 1];
+          else x = sacc[n][kk >> 1][8 * (kk & 1) + e];
+          const float pe = fast_exp2(fmaf(x, c, -mc));
           l_part[n][e & 1] += pe;
           pv[e] = pe;
         }
@@ -934,6 +985,7 @@ AttnParams make_params(const void* q, const void* k, const void* v, void* o, int
   p.offset = (int)(Sk - Sq);
   p.scale = scale;
   p.ref_div = (float)(1.0 / (double)scale);
+  p.ref_rcp = 1.0f / p.ref_div;
   p.c_fast = scale * kLog2e;
   p.softcap = softcap;
   p.inv_softcap = softcap > 0.f ? 1.0f / softcap : 0.f;

@@ -18,6 +18,7 @@ LIB_PATH = Path(os.environ.get("DGG_LIBRARY", Path(__file__).resolve().parent / 
 DGG_F32, DGG_F16, DGG_BF16 = 0, 1, 2
 ATTN_CAUSAL = 0x1
 ATTN_REF_ROUNDING = 0x2
+ATTN_LSE_BASE2 = 0x4
 
 _DTYPE_CODE = {torch.float32: DGG_F32, torch.float16: DGG_F16, torch.bfloat16: DGG_BF16}
 

@@ -21,9 +21,10 @@ def _check_bshd(name: str, t: torch.Tensor):
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool = True, softcap: float = 0.0,
               window: int = 0, scale: float | None = None, return_lse: bool = False, ref_rounding: bool = False,
-              out: torch.Tensor | None = None):
+              out: torch.Tensor | None = None, lse_base2: bool = False):
     """Fused attention forward. q [B, Sq, Hq, D]; k, v [B, Sk, Hkv, D]; returns out [B, Sq, Hq, D] (q.dtype)
-    and, with return_lse, lse [B, Hq, Sq] fp32 (natural log).
+    and, with return_lse, lse [B, Hq, Sq] fp32 (natural log; base 2 with lse_base2, the form
+    attention_colsum(..., lse_base2=True) reads fastest).
 
     Semantics of Attn.forward / Gemma2.forward (deepgengraph_exp/cases/kernels/attn.py:18-34,
     gemma2.py:19-38): scores = q.k^T * scale (default 1/sqrt(D)), optional softcap*tanh(scores/softcap),
@@ -47,7 +48,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool
             raise RuntimeError("attention: out must match q in shape and dtype")
     lse = torch.empty(B, Hq, Sq, dtype=torch.float32, device=q.device) if return_lse else None
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
-    flags = (_lib.ATTN_CAUSAL if causal else 0) | (_lib.ATTN_REF_ROUNDING if ref_rounding else 0)
+    flags = ((_lib.ATTN_CAUSAL if causal else 0) | (_lib.ATTN_REF_ROUNDING if ref_rounding else 0)
+             | (_lib.ATTN_LSE_BASE2 if lse_base2 else 0))
     strides = _lib.int64_array([*q.stride()[:3], *k.stride()[:3], *v.stride()[:3], *out.stride()[:3]])
     _lib.call("dgg_attn_prefill", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out), _lib.ptr(lse), B, Sq, Sk,
               Hq, Hkv, D, strides, scale, float(softcap or 0.0), int(window or 0), flags, _lib.dtype_code(q.dtype),
@@ -57,9 +59,9 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool
 
 def attention_colsum(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor, *, causal: bool = True,
                      softcap: float = 0.0, window: int = 0, scale: float | None = None,
-                     ref_rounding: bool = False) -> torch.Tensor:
+                     ref_rounding: bool = False, lse_base2: bool = False) -> torch.Tensor:
     """Column sums of the softmax probabilities over the query axis, per query head: [B, Hq, Sk] fp32, recomputed
-    from q, k and the lse written by attention(..., return_lse=True) with the same options."""
+    from q, k and the lse written by attention(..., return_lse=True) with the same options (lse_base2 included)."""
     dev = _lib.require_gpu(q, k, lse)
     _check_bshd("q", q)
     _check_bshd("k", k)
@@ -69,7 +71,8 @@ def attention_colsum(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor, *, cau
         raise RuntimeError(f"attention_colsum: lse must be contiguous fp32 [{B}, {Hq}, {Sq}]")
     colsum = torch.empty(B, Hq, Sk, dtype=torch.float32, device=q.device)
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
-    flags = (_lib.ATTN_CAUSAL if causal else 0) | (_lib.ATTN_REF_ROUNDING if ref_rounding else 0)
+    flags = ((_lib.ATTN_CAUSAL if causal else 0) | (_lib.ATTN_REF_ROUNDING if ref_rounding else 0)
+             | (_lib.ATTN_LSE_BASE2 if lse_base2 else 0))
     strides = _lib.int64_array([*q.stride()[:3], *k.stride()[:3]])
     _lib.call("dgg_attn_colsum", _lib.ptr(q), _lib.ptr(k), _lib.ptr(lse), _lib.ptr(colsum), B, Sq, Sk, Hq, Hkv, D,
               strides, scale, float(softcap or 0.0), int(window or 0), flags, _lib.dtype_code(q.dtype),
@@ -82,8 +85,8 @@ def h2o_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, ref_roun
     probability column sums h2o_score [B, Hkv, Sk]. Two launches: the forward kernel (which also writes the row
     lse) and the column-sum kernel. With GQA the per-query-head sums are averaged over each KV group (the
     convention of roco.py:40-41)."""
-    out, lse = attention(q, k, v, causal=True, return_lse=True, ref_rounding=ref_rounding)
-    colsum = attention_colsum(q, k, lse, causal=True, ref_rounding=ref_rounding)
+    out, lse = attention(q, k, v, causal=True, return_lse=True, ref_rounding=ref_rounding, lse_base2=True)
+    colsum = attention_colsum(q, k, lse, causal=True, ref_rounding=ref_rounding, lse_base2=True)
     Hq, Hkv = q.shape[2], k.shape[2]
     if Hq != Hkv:
         colsum = colsum.view(q.shape[0], Hkv, Hq // Hkv, -1).mean(dim=2)

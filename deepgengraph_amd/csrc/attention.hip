@@ -44,6 +44,7 @@ struct AttnParams {
   int causal;
   int window;    // 0 = none
   int offset;    // Sk - Sq (bottom-right aligned causal mask)
+  int lse_base2;  // lse written / read in base 2 (DGG_ATTN_LSE_BASE2)
   float scale;
   float ref_div;  // 1 / scale rounded to fp32 (== fp32 sqrt(D) for the usual scale): the reference divides
                   // the rounded scores by it
@@ -390,7 +391,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D
     }
     if (p.lse != nullptr && g == 0) {
       const float lse2 = m_run == -INFINITY ? -INFINITY : m_run * c + fast_log2(l_tot);
-      p.lse[(int64_t)bh * p.Sq + qi] = lse2 * kLn2;
+      p.lse[(int64_t)bh * p.Sq + qi] = p.lse_base2 ? lse2 : lse2 * kLn2;
     }
   }
 }
@@ -725,7 +726,7 @@ attn_fwd_d128_kernel(AttnParams p) {
       }
       if (p.lse != nullptr && g == 0) {
         const float lse2 = m_run[n] == -INFINITY ? -INFINITY : m_run[n] * c + fast_log2(l_tot);
-        p.lse[(int64_t)bh * p.Sq + qi] = lse2 * kLn2;
+        p.lse[(int64_t)bh * p.Sq + qi] = p.lse_base2 ? lse2 : lse2 * kLn2;
       }
     }
   }
@@ -798,7 +799,7 @@ __global__ void __launch_bounds__(kThreads) attn_colsum_kernel(AttnParams p) {
     if (tid < kCBQ) {
       const int qg = qb + tid;
       // Rows past the end get +inf so that their probability is exp2(-inf) = 0.
-      lreg = qg < p.Sq ? lsep[qg] * kLog2e : INFINITY;
+      lreg = qg < p.Sq ? (p.lse_base2 ? lsep[qg] : lsep[qg] * kLog2e) : INFINITY;
     }
   };
   auto store_tile = [&](int buf) {
@@ -871,6 +872,207 @@ __global__ void __launch_bounds__(kThreads) attn_colsum_kernel(AttnParams p) {
   if (g == 0 && kj < p.Sk) p.colsum[(int64_t)bh * p.Sk + kj] = col;
 }
 
+// ------------------------------------------------------------------------------------------------
+// Column-sum kernel for head_dim 128. A workgroup of NW waves owns 32*NW keys; wave w keeps keys
+// k0 + 32w .. + 31 in VGPRs as the B operand. Query tiles of BQ rows stream through an NSTAGE ring in LDS
+// with the forward's swizzled layout and direct-to-LDS copies (the Q tile takes the place of the K tile),
+// each stage followed by the BQ lse values of its rows (global_load_lds_dword, issued by the last wave).
+// S (BQ x 32) = Q . K^T puts one key per lane: accumulator register j of block mb holds query row
+// 32mb + 8(j/4) + 4(lane/32) + j%4, so each lane sums its key's column over its rows, and the partner
+// lane (lane ^ 32) adds the other half at the end.
+// ------------------------------------------------------------------------------------------------
+__device__ __forceinline__ void dma4(uint32_t lds, const void* vaddr) {
+  // lane l's 4 bytes land at LDS byte address lds + 4*l (lanes switched off by EXEC write nothing)
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(vaddr)
+               : "memory", "m0");
+}
+
+template <typename T, int NW, int BQ, int NSTAGE, bool MASK, bool SOFTCAP, bool REFROUND, bool LSE2>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+attn_colsum_d128_kernel(AttnParams p) {
+  using namespace d128;
+  typedef typename T::scalar S;
+  typedef typename T::vec8 V8;
+  constexpr int BK = 32 * NW;                // keys per workgroup
+  constexpr int QT_B = (BQ / 4) * GROUP_B;   // bytes of one Q tile
+  constexpr int STAGE_B = QT_B + 4 * BQ;     // Q tile, then its BQ lse values
+  constexpr int GPW = (BQ / 4) / NW;         // 4-row groups of a Q tile copied by each wave
+  constexpr int NLSE = BQ / 64;              // lse copies per tile (last wave only)
+  constexpr int NMB = BQ / 32;
+  static_assert(GPW >= 1 && GPW * NW == BQ / 4, "Q tile groups must split over the waves");
+  static_assert(BQ % 64 == 0 && QT_B % 16 == 0, "tile shape");
+  __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * STAGE_B];
+
+  int kt, bh;
+  map_block(p.n_tiles, p.B * p.Hq, false, kt, bh);
+  const int b = bh / p.Hq, h = bh - b * p.Hq;
+  const int hk = h / p.group;
+  const int tid = threadIdx.x, lane = tid & 63, r = lane & 31, g = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int k0 = kt * BK;
+  const int kw0 = k0 + 32 * w;  // first key of this wave
+  const int kj = kw0 + r;       // this lane's key
+
+  const S* kp = static_cast<const S*>(p.k) + b * p.k_sb + hk * p.k_sh;
+  const char* qp = reinterpret_cast<const char*>(static_cast<const S*>(p.q) + b * p.q_sb + h * p.q_sh);
+  const int64_t q_ss_b = p.q_ss * (int64_t)sizeof(S);
+  const float* lsep = p.lse + (int64_t)bh * p.Sq;
+
+  V8 kf[D / 16];
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) {
+    if (kj < p.Sk) kf[kk] = ld16<V8>(kp + (int64_t)kj * p.k_ss + 16 * kk + 8 * g);
+    else kf[kk] = V8{};
+  }
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(kf[kk]));  // see the forward kernel
+
+  // Query tiles that see any key of the workgroup, and of this wave.
+  const int k_last = min(k0 + BK, p.Sk) - 1;
+  int q_begin = 0, q_end = p.Sq;
+  if (p.causal) q_begin = max(0, k0 - p.offset);
+  if (p.window > 0) q_end = min(p.Sq, k_last - p.offset + p.window);
+  const int t_begin = q_begin / BQ;
+  const int t_end = q_end > q_begin ? (q_end + BQ - 1) / BQ : t_begin;
+  int wt_begin = t_begin, wt_end = t_begin;  // empty for a wave whose keys all lie past Sk
+  if (kw0 < p.Sk) {
+    const int wk_last = min(kw0 + 32, p.Sk) - 1;
+    int wq_begin = 0, wq_end = p.Sq;
+    if (p.causal) wq_begin = max(0, kw0 - p.offset);
+    if (p.window > 0) wq_end = min(p.Sq, wk_last - p.offset + p.window);
+    if (wq_end > wq_begin) {
+      wt_begin = wq_begin / BQ;
+      wt_end = (wq_end + BQ - 1) / BQ;
+    }
+  }
+  // Tiles [t_full0, t_full1) need no mask for this wave: every row < Sq sees all 32 keys.
+  int t_full0 = t_begin, t_full1 = t_end;
+  if constexpr (MASK) {
+    if (p.causal) {
+      const int a = kw0 + 31 - p.offset;  // first query row that sees the wave's last key
+      t_full0 = a <= 0 ? t_begin : min(t_end, max(t_begin, (a + BQ - 1) / BQ));
+    }
+    if (p.window > 0) {
+      const int last = kw0 + p.window - p.offset - 1;  // last query row that sees the wave's first key
+      t_full1 = last < 0 ? t_full0 : min(t_end, (last + 1) / BQ);
+    }
+  }
+  if (t_full1 * BQ > p.Sq) t_full1 = p.Sq / BQ;  // ragged last tile
+  if (t_full1 < t_full0) t_full1 = t_full0;
+
+  // Direct-load lane constants (as the forward's K tiles).
+  const int rr = lane >> 4;
+  const uint32_t src_chunk = (uint32_t)((lane & 15) ^ (rr << 2));
+  uint32_t q_voff = (uint32_t)(rr * q_ss_b) + src_chunk * 16u;
+  asm volatile("" : "+v"(q_voff));
+  const uint32_t smem_base = (uint32_t)(size_t)((lds_char*)smem);
+
+  auto issue = [&](int t) {
+    const uint32_t stage = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B);
+    const uint32_t qdst = stage + (uint32_t)(GPW * w * GROUP_B);
+    const int row0 = t * BQ + 4 * GPW * w;
+    if ((t + 1) * BQ <= p.Sq) {
+      const char* qb = qp + (int64_t)row0 * q_ss_b;
+#pragma unroll
+      for (int j = 0; j < GPW; ++j) dma16(qdst + j * GROUP_B, qb + 4 * j * q_ss_b, q_voff);
+    } else {  // ragged last tile: rows past the end re-read the last row (masked)
+#pragma unroll
+      for (int j = 0; j < GPW; ++j) {
+        const int64_t row = min(row0 + 4 * j + rr, p.Sq - 1);
+        dma16(qdst + j * GROUP_B, qp + row * q_ss_b + src_chunk * 16);
+      }
+    }
+    if (w == NW - 1) {
+#pragma unroll
+      for (int i = 0; i < NLSE; ++i) dma4(stage + QT_B + 256 * i, lsep + min(t * BQ + 64 * i + lane, p.Sq - 1));
+    }
+  };
+
+  // Q fragment (row 32mb + r, chunk 2kk + g) addressing, as the forward's K fragments.
+  const int s4 = r & 3;
+  const uint32_t q_lane = (uint32_t)((r >> 2) * GROUP_B + s4 * ROW_B + 16 * g);
+  uint32_t xq[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xq[i] = q_lane + 64u * (uint32_t)(i ^ s4);
+
+  constexpr bool PK = REFROUND && !SOFTCAP && std::is_same<T, F16>::value;
+  const float c = PK ? kLog2e : score_coeff<SOFTCAP, REFROUND>(p);
+  float col = 0.f;
+
+  auto tile = [&](const int t, auto masked) {
+    const uint32_t st = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B);
+    f32x16 sacc[NMB];
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) sacc[mb] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb) {
+        const V8 a = lds_read<V8>(st + xq[kk >> 1] + mb * 8 * GROUP_B + 32 * (kk & 1));
+        sacc[mb] = mfma32(a, kf[kk], sacc[mb]);
+      }
+    }
+    // Visibility of (row o of the tile, this lane's key): causal rel >= 0, window rel < window, row < Sq.
+    const int rel0 = t * BQ + 4 * g + p.offset - kj;
+    const int rows_left = p.Sq - t * BQ - 4 * g;
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) {
+      f32x4 lv[4];
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) lv[jq] = lds_read<f32x4>(st + QT_B + 4 * (32 * mb + 8 * jq + 4 * g));
+      f16x2 hs[8];
+      if constexpr (PK) {
+#pragma unroll
+        for (int jp = 0; jp < 8; ++jp) hs[jp] = ref_scores_f16(sacc[mb][2 * jp], sacc[mb][2 * jp + 1], p);
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float x;
+        if constexpr (PK) x = (float)hs[j >> 1][j & 1];
+        else x = score_value<T, SOFTCAP, REFROUND>(sacc[mb][j], p);
+        const float l2 = LSE2 ? lv[j >> 2][j & 3] : lv[j >> 2][j & 3] * kLog2e;
+        float pe = fast_exp2(fmaf(x, c, -l2));
+        if constexpr (decltype(masked)::value) {
+          const int o = 32 * mb + 8 * (j >> 2) + (j & 3);
+          bool ok = o < rows_left;
+          if constexpr (MASK) {
+            if (p.causal) ok = ok && rel0 + o >= 0;
+            if (p.window > 0) ok = ok && rel0 + o < p.window;
+          }
+          pe = ok ? pe : 0.f;
+        }
+        col += pe;
+      }
+    }
+  };
+
+#pragma unroll
+  for (int i = 0; i < NSTAGE - 1; ++i)
+    if (t_begin + i < t_end) issue(t_begin + i);
+  auto step = [&](const int t, auto masked) {
+    // Tiles t+1 .. t+after may stay in flight; the last wave issues NLSE more copies per tile.
+    const int after = min(NSTAGE - 2, t_end - 1 - t);
+    if (w == NW - 1) {
+      if (NSTAGE >= 4 && after >= 2) wait_vmem<2 * (GPW + NLSE)>();
+      else if (NSTAGE >= 3 && after >= 1) wait_vmem<GPW + NLSE>();
+      else wait_vmem<0>();
+    } else {
+      if (NSTAGE >= 4 && after >= 2) wait_vmem<2 * GPW>();
+      else if (NSTAGE >= 3 && after >= 1) wait_vmem<GPW>();
+      else wait_vmem<0>();
+    }
+    __syncthreads();
+    if (t + NSTAGE - 1 < t_end) issue(t + NSTAGE - 1);
+    if (t >= wt_begin && t < wt_end) tile(t, masked);
+  };
+  for (int t = t_begin; t < t_full0; ++t) step(t, std::true_type{});
+  for (int t = t_full0; t < t_full1; ++t) step(t, std::false_type{});
+  for (int t = t_full1; t < t_end; ++t) step(t, std::true_type{});
+
+  col += __shfl_xor(col, 32, 64);
+  if (g == 0 && kj < p.Sk) p.colsum[(int64_t)bh * p.Sk + kj] = col;
+}
+
 template <typename T, int D, int BN, bool MASK, bool SOFTCAP, bool REFROUND>
 void launch_fwd(const AttnParams& p, hipStream_t st) {
   const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
@@ -917,10 +1119,30 @@ void pick_fwd(const AttnParams& p, bool ref, hipStream_t st) {
     else pick_fwd_ref<T, D, false, false>(p, ref, st);
   }
 }
+// head_dim 128 column sums (measured on MI355X, config 4): 8 waves x 32 keys, 128-row query tiles, 2 stages.
+constexpr int kC128NW = 8, kC128BQ = 128, kC128NS = 2;
+constexpr int kC128BK = 32 * kC128NW;  // keys per workgroup (head_dim 128)
+
+template <typename T, bool MASK, bool SOFTCAP, bool REFROUND>
+void launch_colsum_d128(const AttnParams& p, hipStream_t st) {
+  const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
+  if (p.lse_base2)
+    hipLaunchKernelGGL((attn_colsum_d128_kernel<T, kC128NW, kC128BQ, kC128NS, MASK, SOFTCAP, REFROUND, true>),
+                       dim3(grid), dim3(64 * kC128NW), 0, st, p);
+  else
+    hipLaunchKernelGGL((attn_colsum_d128_kernel<T, kC128NW, kC128BQ, kC128NS, MASK, SOFTCAP, REFROUND, false>),
+                       dim3(grid), dim3(64 * kC128NW), 0, st, p);
+}
+
 template <typename T, int D, bool MASK, bool SOFTCAP>
 void pick_col_ref(const AttnParams& p, bool ref, hipStream_t st) {
-  if (ref) launch_colsum<T, D, MASK, SOFTCAP, true>(p, st);
-  else launch_colsum<T, D, MASK, SOFTCAP, false>(p, st);
+  if constexpr (D == 128) {
+    if (ref) launch_colsum_d128<T, MASK, SOFTCAP, true>(p, st);
+    else launch_colsum_d128<T, MASK, SOFTCAP, false>(p, st);
+  } else {
+    if (ref) launch_colsum<T, D, MASK, SOFTCAP, true>(p, st);
+    else launch_colsum<T, D, MASK, SOFTCAP, false>(p, st);
+  }
 }
 template <typename T, int D>
 void pick_col(const AttnParams& p, bool ref, hipStream_t st) {
@@ -981,6 +1203,7 @@ AttnParams make_params(const void* q, const void* k, const void* v, void* o, int
   p.Hkv = (int)Hkv;
   p.group = (int)(Hq / Hkv);
   p.causal = (flags & DGG_ATTN_CAUSAL) ? 1 : 0;
+  p.lse_base2 = (flags & DGG_ATTN_LSE_BASE2) ? 1 : 0;
   p.window = (int)window;
   p.offset = (int)(Sk - Sq);
   p.scale = scale;
@@ -1041,7 +1264,8 @@ extern "C" int dgg_attn_colsum(const void* q, const void* k, const float* lse, f
   p.colsum = colsum;
   p.q_sb = strides[0]; p.q_ss = strides[1]; p.q_sh = strides[2];
   p.k_sb = strides[3]; p.k_ss = strides[4]; p.k_sh = strides[5];
-  p.n_tiles = (int)((Sk + kCBK - 1) / kCBK);
+  const int64_t bk = D == 128 ? kC128BK : kCBK;
+  p.n_tiles = (int)((Sk + bk - 1) / bk);
   const bool ref = (flags & DGG_ATTN_REF_ROUNDING) != 0;
   hipStream_t st = dgg::as_stream(stream);
   if (dtype == DGG_BF16) {

@@ -193,64 +193,80 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* w
   return before + inc - v;
 }
 
+// PER: elements per thread kept in registers (n <= PER * 1024). Histograms are per wave (no atomics
+// shared across waves); the digit of each pass is found by a 256-thread suffix scan over the bins.
+template <int PER>
 __global__ void __launch_bounds__(kTopkThreads) topk_kernel(const float* __restrict__ scores, int n, int k,
                                                              int64_t* __restrict__ out) {
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t wsum[kTopkThreads / 64];
+  constexpr int NWV = kTopkThreads / 64;
+  __shared__ uint32_t hist[NWV][256];
+  __shared__ uint32_t wsum[NWV];
   __shared__ uint32_t sel_digit, sel_remaining;
   const float* x = scores + (int64_t)blockIdx.x * n;
   int64_t* o = out + (int64_t)blockIdx.x * k;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int per = (n + kTopkThreads - 1) / kTopkThreads;
-  const int seg0 = min(n, tid * per), seg1 = min(n, seg0 + per);
+  const int seg0 = min(n, tid * per), cnt = min(n, seg0 + per) - seg0;
+
+  uint32_t key[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) key[j] = j < cnt ? order_key(x[seg0 + j]) : 0u;
 
   uint32_t prefix = 0, pmask = 0, remaining = (uint32_t)k;
   for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int i = tid; i < 256; i += kTopkThreads) hist[i] = 0;
+    for (int i = tid; i < NWV * 256; i += kTopkThreads) (&hist[0][0])[i] = 0u;
     __syncthreads();
-    for (int i = seg0; i < seg1; ++i) {
-      const uint32_t key = order_key(x[i]);
-      if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (j < cnt && (key[j] & pmask) == prefix) atomicAdd(&hist[wv][(key[j] >> shift) & 255u], 1u);
+    __syncthreads();
+    // Thread t < 256 takes bin 255 - t: an inclusive scan over t counts the candidates in bins >= 255 - t.
+    uint32_t c = 0, incl = 0;
+    if (tid < 256) {
+#pragma unroll
+      for (int w2 = 0; w2 < NWV; ++w2) c += hist[w2][255 - tid];
+      incl = c;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t t = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += t;
+      }
+      if (lane == 63) wsum[wv] = incl;
     }
     __syncthreads();
-    if (tid == 0) {
-      uint32_t cum = 0;
-      int dsel = 0;
-      for (int d = 255; d >= 0; --d) {
-        if (cum + hist[d] >= remaining) {
-          dsel = d;
-          break;
-        }
-        cum += hist[d];
+    if (tid < 256) {
+      uint32_t base = 0;
+      for (int w2 = 0; w2 < wv; ++w2) base += wsum[w2];
+      const uint32_t hi = base + incl, lo = hi - c;  // candidates in bins above / from this bin
+      if (lo < remaining && hi >= remaining) {      // exactly one bin: the k-th largest lies in it
+        sel_digit = 255u - (uint32_t)tid;
+        sel_remaining = remaining - lo;
       }
-      sel_digit = (uint32_t)dsel;
-      sel_remaining = remaining - cum;
     }
     __syncthreads();
     prefix |= sel_digit << shift;
     pmask |= 255u << shift;
     remaining = sel_remaining;
-    __syncthreads();
   }
   // prefix = K*; `remaining` elements equal to K* are still to be taken, lowest index first.
-  uint32_t eq = 0;
-  for (int i = seg0; i < seg1; ++i) eq += order_key(x[i]) == prefix;
+  uint32_t eq = 0, gt = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    eq += j < cnt && key[j] == prefix;
+    gt += j < cnt && key[j] > prefix;
+  }
   uint32_t tot;
   const uint32_t eq_before = block_exclusive_scan(eq, wsum, tot);
-  uint32_t sel = 0, eq_seen = eq_before;
-  for (int i = seg0; i < seg1; ++i) {
-    const uint32_t key = order_key(x[i]);
-    if (key > prefix) ++sel;
-    else if (key == prefix) sel += (eq_seen++ < remaining);
-  }
-  const uint32_t pos0 = block_exclusive_scan(sel, wsum, tot);
-  uint32_t pos = pos0;
-  eq_seen = eq_before;
-  for (int i = seg0; i < seg1; ++i) {
-    const uint32_t key = order_key(x[i]);
-    bool take = key > prefix;
-    if (key == prefix) take = eq_seen++ < remaining;
-    if (take && pos < (uint32_t)k) o[pos++] = i;
+  const uint32_t eq_take = eq_before >= remaining ? 0u : min(eq, remaining - eq_before);
+  uint32_t pos = block_exclusive_scan(gt + eq_take, wsum, tot);
+  uint32_t eq_seen = eq_before;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    if (j < cnt) {
+      bool take = key[j] > prefix;
+      if (key[j] == prefix) take = eq_seen++ < remaining;
+      if (take && pos < (uint32_t)k) o[pos++] = seg0 + j;
+    }
   }
 }
 
@@ -328,7 +344,10 @@ extern "C" int dgg_topk_indices(const float* scores, int64_t rows, int64_t n, in
               (long long)k, (long long)n);
   if (rows == 0) return DGG_OK;
   DGG_REQUIRE(scores && out_idx, DGG_ERR_NULL, "topk_indices: null pointer");
-  hipLaunchKernelGGL(topk_kernel, dim3((unsigned)rows), dim3(kTopkThreads), 0, dgg::as_stream(stream), scores, (int)n,
-                     (int)k, out_idx);
+  const dim3 grid((unsigned)rows), block(kTopkThreads);
+  hipStream_t st = dgg::as_stream(stream);
+  if (n <= 4 * kTopkThreads) hipLaunchKernelGGL(topk_kernel<4>, grid, block, 0, st, scores, (int)n, (int)k, out_idx);
+  else if (n <= 16 * kTopkThreads) hipLaunchKernelGGL(topk_kernel<16>, grid, block, 0, st, scores, (int)n, (int)k, out_idx);
+  else hipLaunchKernelGGL(topk_kernel<64>, grid, block, 0, st, scores, (int)n, (int)k, out_idx);
   return dgg::check_launch("topk_indices");
 }

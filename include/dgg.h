@@ -43,6 +43,10 @@ enum dgg_status {
  * (Q.K^T result, the 1/sqrt(D) scaling, each soft-cap step) before the fp32 softmax. Costs a few VALU
  * ops per score; used where downstream selection (H2O top-k) depends on exact probabilities. */
 #define DGG_ATTN_REF_ROUNDING 0x2u
+/* lse in base 2 (log2 of the row sum of 2^(scores*log2(e)), i.e. the natural lse times log2(e)):
+ * dgg_attn_prefill writes it so and dgg_attn_colsum reads it so. Saves one multiply per score in the
+ * column-sum pass when the caller only hands the lse from one to the other (as H2O does). */
+#define DGG_ATTN_LSE_BASE2 0x4u
 
 int dgg_abi_version(void);
 const char* dgg_last_error(void);
@@ -95,7 +99,7 @@ int dgg_rotary_embedding_online(const int32_t* positions, void* query, void* key
  *   mask (flags & DGG_ATTN_CAUSAL: key j visible iff j <= i + Sk - Sq; window > 0: also iff
  *   i + Sk - Sq - j < window); p = softmax_j(scores) in fp32; o = p . v.
  * lse (optional, may be NULL): fp32 [B, Hq, Sq] contiguous, natural-log log-sum-exp of the masked
- * scaled scores; -inf for a row with no visible key (its o row is NaN, as the reference's softmax of an
+ * scaled scores (base 2 with DGG_ATTN_LSE_BASE2); -inf for a row with no visible key (its o row is NaN, as the reference's softmax of an
  * all -inf row). strides: 12 int64 = q{b,s,h}, k{b,s,h}, v{b,s,h}, o{b,s,h}. */
 int dgg_attn_prefill(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t Sq,
                      int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides, float scale,
@@ -103,7 +107,7 @@ int dgg_attn_prefill(const void* q, const void* k, const void* v, void* o, float
 
 /* H2O column sums (deepgengraph_exp/cases/kernels/h2o.py:35-36): colsum[b,h,j] = sum_i p[b,h,i,j] with p
  * the fp32 probabilities of dgg_attn_prefill, recomputed from q, k and the lse it wrote (same scale,
- * softcap, window and flags). colsum: fp32 [B, Hq, Sk] contiguous. strides: 6 int64 = q{b,s,h}, k{b,s,h}. */
+ * softcap, window and flags, DGG_ATTN_LSE_BASE2 included). colsum: fp32 [B, Hq, Sk] contiguous. strides: 6 int64 = q{b,s,h}, k{b,s,h}. */
 int dgg_attn_colsum(const void* q, const void* k, const float* lse, float* colsum, int64_t B, int64_t Sq,
                     int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides, float scale,
                     float softcap, int64_t window, uint32_t flags, int dtype, void* stream);

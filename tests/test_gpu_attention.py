@@ -111,21 +111,37 @@ def test_h2o_matches_oracle(gpu, S, H, D, sinks):
     np.testing.assert_array_equal(A.topk_indices(ref_cs.to(gpu), kk).cpu().numpy(), osel.topk_indices(ref_cs.numpy(), kk))
 
 
-def test_colsum_variants(gpu):
-    # column sums with soft-cap, window and GQA (per query head) against sums of the oracle's probabilities
-    B, S, Hq, Hkv, D = 1, 200, 4, 2, 64
-    q, k, v = _qkv(B, S, S, Hq, Hkv, D, torch.bfloat16, 77)
-    out, lse = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), softcap=20.0, window=50, return_lse=True)
-    cs = A.attention_colsum(q.to(gpu), k.to(gpu), lse, softcap=20.0, window=50).cpu()
-    # oracle probabilities in fp32 from the oracle's scores
-    qt, kt = q.transpose(1, 2).float(), k.transpose(1, 2).repeat_interleave(2, 1).float()
+@pytest.mark.parametrize("D,Sq,Sk,causal,window,softcap,dtype,base2", [
+    (64, 200, 200, True, 50, 20.0, torch.bfloat16, False),
+    (128, 200, 200, True, 50, 20.0, torch.bfloat16, False),
+    (128, 333, 517, True, 0, 0.0, torch.float16, True),
+    (128, 517, 333, True, 0, 0.0, torch.bfloat16, False),   # Sq > Sk: leading rows see no key
+    (128, 300, 300, False, 0, 0.0, torch.float16, True),
+    (128, 640, 640, True, 100, 0.0, torch.float16, True),
+    (256, 160, 160, True, 0, 30.0, torch.bfloat16, False),
+])
+def test_colsum_variants(gpu, D, Sq, Sk, causal, window, softcap, dtype, base2):
+    # column sums (soft-cap, window, GQA, Sq != Sk, both lse forms) against sums of fp32 softmax probabilities
+    B, Hq, Hkv = 1, 4, 2
+    q, k, v = _qkv(B, Sq, Sk, Hq, Hkv, D, dtype, 77 + D + Sq)
+    kw = dict(causal=causal, softcap=softcap, window=window, lse_base2=base2)
+    out, lse = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), return_lse=True, **kw)
+    cs = A.attention_colsum(q.to(gpu), k.to(gpu), lse, **kw).cpu()
+    qt, kt = q.transpose(1, 2).float(), k.transpose(1, 2).repeat_interleave(Hq // Hkv, 1).float()
     s = torch.matmul(qt, kt.transpose(-1, -2)) / math.sqrt(D)
-    s = 20.0 * torch.tanh(s / 20.0)
-    i = torch.arange(S).view(S, 1)
-    j = torch.arange(S).view(1, S)
-    s = s.masked_fill((j > i) | (i - j >= 50), float("-inf"))
-    ref = torch.softmax(s, -1).sum(2)
-    assert_close(cs, ref, 1e-3, 1e-2, "colsum softcap/window/gqa (kernel keeps fp32 scores, oracle fp32)")
+    if softcap:
+        s = softcap * torch.tanh(s / softcap)
+    i = torch.arange(Sq).view(Sq, 1) + (Sk - Sq)
+    j = torch.arange(Sk).view(1, Sk)
+    hidden = torch.zeros(Sq, Sk, dtype=torch.bool)
+    if causal:
+        hidden |= j > i
+    if window:
+        hidden |= i - j >= window
+    s = s.masked_fill(hidden, float("-inf"))
+    ref = torch.softmax(s, -1).nan_to_num(0.0).sum(2)   # rows that see no key contribute nothing
+    what = f"colsum D{D} Sq{Sq} Sk{Sk} causal{causal} w{window} sc{softcap} {dtype} base2={base2}"
+    assert_close(cs, ref, 1e-3, 1e-2, what + " (kernel keeps fp32 scores, reference fp32)")
 
 
 def test_topk_kernel_golden_and_ties(gpu):

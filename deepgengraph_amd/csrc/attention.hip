@@ -397,21 +397,24 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D
 }
 
 // ------------------------------------------------------------------------------------------------
-// Forward kernel for head_dim 128: 4 waves x 64 query rows (two 32-row MFMA column blocks per wave, so every K
-// and V fragment read from LDS feeds two MFMAs), one wave per SIMD (accumulators may live in AGPRs). K/V tiles
-// of 64 keys are copied global -> LDS by the direct-to-LDS loads of gfx950 (no VGPR staging, no LDS store
-// instructions) into a 4-stage ring, so three tiles are in flight while one is computed, with one barrier per
-// tile. Each 16-byte chunk c of tile row r sits at
-//     (r/4)*GROUP_B + (r%4)*ROW_B + 16*(c ^ 4*(r%4))        (4-row groups padded by 16 bytes)
+// Forward kernel for head_dim 128 and 256 ("DMA kernel"). NW waves of 32*NQB query rows each; K/V tiles of BN
+// keys are copied global -> LDS by the direct-to-LDS loads of gfx950 (no VGPR staging, no LDS store
+// instructions) into an NSTAGE ring, with one barrier per tile. head_dim 128 runs 8 waves at two per SIMD;
+// head_dim 256 (Q 64 + O 128 VGPRs per lane) runs 4 waves at one per SIMD. Each 16-byte chunk c of tile row r
+// sits at
+//     (r/4)*GROUP_B + (r%4)*ROW_B + 16*(c ^ 4*(r%4))        (ROW_B = 2*D bytes, 4-row groups padded by 16 bytes)
 // which keeps both the K fragment reads (16 lanes, 16 rows, one chunk) and the V transposing reads (4 rows x
 // 4 chunks per 16-lane group) on distinct LDS banks; the direct loads write that layout by fetching, for LDS
-// position p of a row, global chunk p ^ 4*(r%4).
+// position p of a row, global chunk p ^ 4*(r%4). One direct load covers 1 KiB: 4 rows of 128 or 2 of 256.
 // ------------------------------------------------------------------------------------------------
-namespace d128 {
-constexpr int D = 128;
-constexpr int ROW_B = D * 2;               // bytes per K/V row
-constexpr int GROUP_B = 4 * ROW_B + 16;    // 4-row group + pad
-}  // namespace d128
+template <int D>
+struct DmaLayout {
+  static constexpr int ROW_B = D * 2;             // bytes per K/V row
+  static constexpr int GROUP_B = 4 * ROW_B + 16;  // 4-row group + pad
+  static constexpr int LPR = ROW_B / 16;          // lanes per row in one direct load
+  static constexpr int RPI = 64 / LPR;            // rows per direct load
+  static constexpr int IPG = 4 / RPI;             // direct loads per 4-row group
+};
 
 typedef __attribute__((address_space(3))) char lds_char;
 
@@ -443,11 +446,12 @@ __device__ __forceinline__ void wait_vmem() {
 }
 
 // NQB: 32-row query blocks per wave (each K / V fragment feeds NQB MFMAs); NW: waves per workgroup; BN: keys
-// per tile; NSTAGE: tiles in the LDS ring.
-template <typename T, int NQB, int NW, int BN, int NSTAGE, bool MASK, bool SOFTCAP, bool REFROUND>
-__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NQB * NW / 4 == 1 ? 1 : 2, 2)))
-attn_fwd_d128_kernel(AttnParams p) {
-  using namespace d128;
+// per tile; NSTAGE: tiles in the LDS ring; OCC: waves per SIMD the register budget is sized for.
+template <typename T, int D, int NQB, int NW, int BN, int NSTAGE, int OCC, bool MASK, bool SOFTCAP, bool REFROUND>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
+attn_fwd_dma_kernel(AttnParams p) {
+  typedef DmaLayout<D> L;
+  constexpr int ROW_B = L::ROW_B, GROUP_B = L::GROUP_B, LPR = L::LPR, RPI = L::RPI, IPG = L::IPG;
   typedef typename T::scalar S;
   typedef typename T::vec8 V8;
   typedef typename T::vec4 V4;
@@ -456,7 +460,7 @@ attn_fwd_d128_kernel(AttnParams p) {
   constexpr int TILE_B = (BN / 4) * GROUP_B;
   constexpr int STAGE_B = 2 * TILE_B;           // K tile, then V tile
   constexpr int GPW = (BN / 4) / NW;            // 4-row groups of a tile copied by each wave (K and V each)
-  constexpr int DMA_PER_TILE = 2 * GPW;         // direct loads per wave per tile
+  constexpr int DMA_PER_TILE = 2 * GPW * IPG;   // direct loads per wave per tile
   static_assert(GPW >= 1 && GPW * NW == BN / 4, "tile groups must split over the waves");
   __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * STAGE_B];
 
@@ -512,13 +516,17 @@ attn_fwd_d128_kernel(AttnParams p) {
     if (p.window > 0) k_lo[n] = max(k_lo[n], qi + p.offset - p.window + 1);
   }
 
-  // Direct-load lane constants: lane l fills LDS position l%16 of row l/16 of a 4-row group, fetching global
-  // chunk (l%16) ^ 4*(l/16).
-  const int rr = lane >> 4;
-  const uint32_t src_chunk = (uint32_t)((lane & 15) ^ (rr << 2));
-  uint32_t k_voff = (uint32_t)(rr * k_ss_b) + src_chunk * 16u;
-  uint32_t v_voff = (uint32_t)(rr * v_ss_b) + src_chunk * 16u;
-  asm volatile("" : "+v"(k_voff), "+v"(v_voff));
+  // Direct-load lane constants: in load i of a 4-row group, lane l fills LDS position l%LPR of group row
+  // i*RPI + l/LPR, fetching global chunk (l%LPR) ^ 4*(group row).
+  uint32_t src_chunk[IPG], k_voff[IPG], v_voff[IPG];
+#pragma unroll
+  for (int i = 0; i < IPG; ++i) {
+    const int grow = i * RPI + lane / LPR;
+    src_chunk[i] = (uint32_t)((lane % LPR) ^ (grow << 2));
+    k_voff[i] = (uint32_t)(grow * k_ss_b) + src_chunk[i] * 16u;
+    v_voff[i] = (uint32_t)(grow * v_ss_b) + src_chunk[i] * 16u;
+    asm volatile("" : "+v"(k_voff[i]), "+v"(v_voff[i]));
+  }
   const uint32_t smem_base = (uint32_t)(size_t)((lds_char*)smem);
 
   // Copies groups GPW*w .. GPW*w + GPW-1 of tile t into stage t % NSTAGE: DMA_PER_TILE loads per wave.
@@ -530,17 +538,21 @@ attn_fwd_d128_kernel(AttnParams p) {
       const char* kb = kp + (int64_t)row0 * k_ss_b;
       const char* vb = vp + (int64_t)row0 * v_ss_b;
 #pragma unroll
-      for (int j = 0; j < GPW; ++j) {
-        dma16(kdst + j * GROUP_B, kb + 4 * j * k_ss_b, k_voff);
-        dma16(vdst + j * GROUP_B, vb + 4 * j * v_ss_b, v_voff);
-      }
+      for (int j = 0; j < GPW; ++j)
+#pragma unroll
+        for (int i = 0; i < IPG; ++i) {
+          dma16(kdst + j * GROUP_B + i * RPI * ROW_B, kb + 4 * j * k_ss_b, k_voff[i]);
+          dma16(vdst + j * GROUP_B + i * RPI * ROW_B, vb + 4 * j * v_ss_b, v_voff[i]);
+        }
     } else {  // ragged last tile: rows past the end re-read the last row (always masked, finite)
 #pragma unroll
-      for (int j = 0; j < GPW; ++j) {
-        const int64_t row = min(row0 + 4 * j + rr, p.Sk - 1);
-        dma16(kdst + j * GROUP_B, kp + row * k_ss_b + src_chunk * 16);
-        dma16(vdst + j * GROUP_B, vp + row * v_ss_b + src_chunk * 16);
-      }
+      for (int j = 0; j < GPW; ++j)
+#pragma unroll
+        for (int i = 0; i < IPG; ++i) {
+          const int64_t row = min(row0 + 4 * j + i * RPI + lane / LPR, p.Sk - 1);
+          dma16(kdst + j * GROUP_B + i * RPI * ROW_B, kp + row * k_ss_b + src_chunk[i] * 16);
+          dma16(vdst + j * GROUP_B + i * RPI * ROW_B, vp + row * v_ss_b + src_chunk[i] * 16);
+        }
     }
   };
 
@@ -549,15 +561,15 @@ attn_fwd_d128_kernel(AttnParams p) {
   // lane part + xv[db] + constant.
   const int s4 = r & 3;
   const uint32_t k_lane = (uint32_t)((r >> 2) * GROUP_B + s4 * ROW_B + 16 * g);
-  uint32_t xk[4];
+  uint32_t xk[D / 32];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) xk[i] = k_lane + 64u * (uint32_t)(i ^ s4);
+  for (int i = 0; i < D / 32; ++i) xk[i] = k_lane + 64u * (uint32_t)(i ^ s4);
   const int m4 = (lane & 15) >> 2, m3 = lane & 3;
   const uint32_t v_lane = (uint32_t)(TILE_B + g * GROUP_B + m4 * ROW_B + 32 * ((lane >> 4) & 1) + 16 * (m3 >> 1) +
                                      8 * (m3 & 1));
-  uint32_t xv[4];
+  uint32_t xv[D / 32];
 #pragma unroll
-  for (int db = 0; db < 4; ++db) xv[db] = v_lane + 64u * (uint32_t)(db ^ m4);
+  for (int db = 0; db < D / 32; ++db) xv[db] = v_lane + 64u * (uint32_t)(db ^ m4);
 
   f32x16 oacc[NQB][D / 32];
   float m_run[NQB], l_part[NQB][2];
@@ -890,7 +902,8 @@ __device__ __forceinline__ void dma4(uint32_t lds, const void* vaddr) {
 template <typename T, int NW, int BQ, int NSTAGE, bool MASK, bool SOFTCAP, bool REFROUND, bool LSE2>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_colsum_d128_kernel(AttnParams p) {
-  using namespace d128;
+  constexpr int D = 128;
+  constexpr int ROW_B = DmaLayout<D>::ROW_B, GROUP_B = DmaLayout<D>::GROUP_B;
   typedef typename T::scalar S;
   typedef typename T::vec8 V8;
   constexpr int BK = 32 * NW;                // keys per workgroup
@@ -1092,8 +1105,22 @@ constexpr int kD128BM = 32 * kD128NQB * kD128NW;  // query rows per workgroup (h
 template <typename T, bool MASK, bool SOFTCAP, bool REFROUND>
 void launch_fwd_d128(const AttnParams& p, hipStream_t st) {
   const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
-  hipLaunchKernelGGL((attn_fwd_d128_kernel<T, kD128NQB, kD128NW, kD128BN, kD128NS, MASK, SOFTCAP, REFROUND>), dim3(grid),
-                     dim3(64 * kD128NW), 0, st, p);
+  hipLaunchKernelGGL((attn_fwd_dma_kernel<T, 128, kD128NQB, kD128NW, kD128BN, kD128NS, 2, MASK, SOFTCAP, REFROUND>),
+                     dim3(grid), dim3(64 * kD128NW), 0, st, p);
+}
+
+// head_dim 256 configuration: 4 waves x 32 rows (one wave per SIMD), DGG_D256_BN-key tiles, 2-stage ring.
+#ifndef DGG_D256_BN
+#define DGG_D256_BN 64
+#endif
+constexpr int kD256NW = 4, kD256BN = DGG_D256_BN, kD256NS = 2;
+constexpr int kD256BM = 32 * kD256NW;
+
+template <typename T, bool MASK, bool SOFTCAP, bool REFROUND>
+void launch_fwd_d256(const AttnParams& p, hipStream_t st) {
+  const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
+  hipLaunchKernelGGL((attn_fwd_dma_kernel<T, 256, 1, kD256NW, kD256BN, kD256NS, 1, MASK, SOFTCAP, REFROUND>),
+                     dim3(grid), dim3(64 * kD256NW), 0, st, p);
 }
 
 template <typename T, int D, bool MASK, bool SOFTCAP>
@@ -1102,6 +1129,9 @@ void pick_fwd_ref(const AttnParams& p, bool ref, hipStream_t st) {
   if constexpr (D == 128) {
     if (ref) launch_fwd_d128<T, MASK, SOFTCAP, true>(p, st);
     else launch_fwd_d128<T, MASK, SOFTCAP, false>(p, st);
+  } else if constexpr (D == 256) {
+    if (ref) launch_fwd_d256<T, MASK, SOFTCAP, true>(p, st);
+    else launch_fwd_d256<T, MASK, SOFTCAP, false>(p, st);
   } else {
     if (ref) launch_fwd<T, D, BN, MASK, SOFTCAP, true>(p, st);
     else launch_fwd<T, D, BN, MASK, SOFTCAP, false>(p, st);
@@ -1233,7 +1263,7 @@ extern "C" int dgg_attn_prefill(const void* q, const void* k, const void* v, voi
   p.k_sb = strides[3]; p.k_ss = strides[4]; p.k_sh = strides[5];
   p.v_sb = strides[6]; p.v_ss = strides[7]; p.v_sh = strides[8];
   p.o_sb = strides[9]; p.o_ss = strides[10]; p.o_sh = strides[11];
-  const int64_t bm = D == 128 ? kD128BM : kBM;
+  const int64_t bm = D == 128 ? kD128BM : D == 256 ? kD256BM : kBM;
   p.n_tiles = (int)((Sq + bm - 1) / bm);
   const bool ref = (flags & DGG_ATTN_REF_ROUNDING) != 0;
   hipStream_t st = dgg::as_stream(stream);

@@ -34,6 +34,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source extra flags. The attention kernels are long unrolled MFMA / LDS-read sequences; LLVM's
+# iterative ILP machine scheduler issues the LDS fragment reads further ahead of the MFMAs that consume them
+# than the default occupancy-driven scheduler (measured on MI355X: +3% prefill at head_dim 128, +10% at 256).
+EXTRA_FLAGS = {
+    "attention.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+}
+
+
 def _hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(exe).exists():
@@ -43,7 +51,7 @@ def _hipcc() -> str:
 
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -491,7 +491,12 @@ attn_fwd_dma_kernel(AttnParams p) {
 #pragma unroll
   for (int n = 0; n < NQB; ++n)
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(qf[n][kk]));
+    for (int kk = 0; kk < D / 16; ++kk) {
+      // At one wave per SIMD (head_dim 256) Q lives in AGPRs (MFMA reads its B operand from there), which
+      // leaves the VGPRs to the S scores and to K / V fragments read ahead of their MFMAs.
+      if constexpr (OCC == 1) asm volatile("" : "+a"(qf[n][kk]));
+      else asm volatile("" : "+v"(qf[n][kk]));
+    }
 
   // Key tiles of the workgroup and of this wave.
   const int q_last = min(q0 + BM, p.Sq) - 1;

@@ -253,7 +253,7 @@ def main():
                    "flops_per_step": pre["flops"], "exact_pair_flops": pre["exact_flops"]},
         "roofline": {"bound": "mfma", "achieved": round(pre["tflops_kern"], 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(pre["tflops_kern"] / PEAK_BF16_TFLOPS, 4),
-                     "traffic": measured_traffic("attn_fwd_d128_kernel"), "kernel_ms": round(pre["kern_ms"], 5)},
+                     "traffic": measured_traffic("attn_fwd_dma_kernel<BF16, 128"), "kernel_ms": round(pre["kern_ms"], 5)},
     }
     line.update(extra)
     if not args.no_cpu_baseline:

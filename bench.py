@@ -140,6 +140,17 @@ def bench_variants(args, dev):
     res["cfg4_h2o_fwd_colsum_topk"] = dict(ms=round(ms, 4),
                                            tflops=round(cfg.reference_flops() / (ms * 1e-3) / 1e12, 1),
                                            frac=round(cfg.reference_flops() / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))
+    # the other selection cases of the reference at config-4 shapes (same inputs; Corm's threshold 1/(i+1))
+    thr = torch.ones(cfg.Sq, cfg.Sk, device=dev) / torch.arange(1, cfg.Sq + 1, device=dev, dtype=torch.float32)[:, None]
+    for name, fn in (("cfg4_roco", lambda: A.roco_attention(q, k, v)),
+                     ("cfg4_snapkv", lambda: A.snapkv_attention(q, k, v)),
+                     ("cfg4_corm", lambda: A.corm_attention(q, k, v, thr))):
+        ms = statistics.mean(_events_time(fn, 5, 1))
+        res[name] = dict(ms=round(ms, 4), tflops=round(cfg.reference_flops() / (ms * 1e-3) / 1e12, 1))
+    idx = A.topk_indices(A.h2o_attention(q, k, v)[1], cfg.topk)
+    ms = statistics.mean(_events_time(lambda: A.kv_gather(k, v, idx), 20, 2))
+    nb = 2 * 2 * idx.numel() * cfg.D * k.element_size()  # K and V rows read once and written once
+    res["cfg4_kv_gather_top256"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1))
     return res
 
 

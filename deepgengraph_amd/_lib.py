@@ -19,6 +19,7 @@ DGG_F32, DGG_F16, DGG_BF16 = 0, 1, 2
 ATTN_CAUSAL = 0x1
 ATTN_REF_ROUNDING = 0x2
 ATTN_LSE_BASE2 = 0x4
+COL_SUM, COL_SUM_SQ, COL_ANY_GE = 0, 1, 2
 
 _DTYPE_CODE = {torch.float32: DGG_F32, torch.float16: DGG_F16, torch.bfloat16: DGG_BF16}
 
@@ -41,6 +42,10 @@ SIGNATURES = {
                                 _i64, _u32, _i32, _vp]),
     "dgg_attn_colsum": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64p, _f32, _f32, _i64,
                                _u32, _i32, _vp]),
+    "dgg_attn_colscore": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                 _i64p, _f32, _f32, _i64, _u32, _i32, _vp]),
+    "dgg_avg_pool1d": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp]),
+    "dgg_kv_gather": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64p, _i32, _vp]),
     "dgg_topk_indices": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp]),
     "dgg_attn_decode_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "dgg_attn_decode": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64p, _i64, _f32,

@@ -93,6 +93,110 @@ def h2o_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, ref_roun
     return out, colsum
 
 
+def attention_colscore(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor, *, epilogue: int,
+                       thr: torch.Tensor | None = None, causal: bool = True, window: int = 0,
+                       scale: float | None = None, ref_rounding: bool = False, lse_base2: bool = False):
+    """Column scores over the query axis from q, k and the forward's lse (same options), per query head [B, Hq, Sk]:
+    epilogue COL_SUM -> sum_i p; COL_SUM_SQ -> (sum_i p, sum_i p^2) (roco.py:43-47); COL_ANY_GE -> bool
+    any_i p[i, j] >= thr[i, j] with thr fp32 [Sq, Sk] (corm.py:35-37)."""
+    dev = _lib.require_gpu(q, k, lse, thr)
+    _check_bshd("q", q)
+    _check_bshd("k", k)
+    B, Sq, Hq, D = q.shape
+    Sk, Hkv = k.shape[1], k.shape[2]
+    if lse.shape != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise RuntimeError(f"attention_colscore: lse must be contiguous fp32 [{B}, {Hq}, {Sq}]")
+    out0 = out1 = anyo = None
+    thr_rs = 0
+    if epilogue == _lib.COL_ANY_GE:
+        if thr is None or thr.dim() != 2 or thr.shape != (Sq, Sk) or thr.dtype != torch.float32 or thr.stride(-1) != 1:
+            raise RuntimeError(f"attention_colscore: thr must be fp32 [{Sq}, {Sk}] with unit column stride")
+        thr_rs = thr.stride(0)
+        anyo = torch.empty(B, Hq, Sk, dtype=torch.uint8, device=q.device)
+    else:
+        out0 = torch.empty(B, Hq, Sk, dtype=torch.float32, device=q.device)
+        if epilogue == _lib.COL_SUM_SQ:
+            out1 = torch.empty(B, Hq, Sk, dtype=torch.float32, device=q.device)
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    flags = ((_lib.ATTN_CAUSAL if causal else 0) | (_lib.ATTN_REF_ROUNDING if ref_rounding else 0)
+             | (_lib.ATTN_LSE_BASE2 if lse_base2 else 0))
+    strides = _lib.int64_array([*q.stride()[:3], *k.stride()[:3]])
+    _lib.call("dgg_attn_colscore", _lib.ptr(q), _lib.ptr(k), _lib.ptr(lse), int(epilogue), _lib.ptr(out0),
+              _lib.ptr(out1), _lib.ptr(anyo), _lib.ptr(thr), thr_rs, B, Sq, Sk, Hq, Hkv, D, strides, scale, 0.0,
+              int(window or 0), flags, _lib.dtype_code(q.dtype), _lib.stream_handle(dev))
+    if epilogue == _lib.COL_ANY_GE:
+        return anyo.view(torch.bool)
+    return (out0, out1) if epilogue == _lib.COL_SUM_SQ else out0
+
+
+def _require_mha(name: str, q: torch.Tensor, k: torch.Tensor):
+    if q.shape[2] != k.shape[2]:
+        raise RuntimeError(f"{name}: the reference case is multi-head attention (head_num == kv_head_num)")
+
+
+def roco_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, ref_rounding: bool = True):
+    """RoCo.forward (deepgengraph_exp/cases/kernels/roco.py:18-48): causal attention, roco_score = sum_i p and
+    roco_sq_score = sum_i p^2 per key, fp32 [B, H, Sk]. MHA, as roco.py:16 asserts."""
+    _require_mha("roco_attention", q, k)
+    out, lse = attention(q, k, v, causal=True, return_lse=True, ref_rounding=ref_rounding, lse_base2=True)
+    s1, s2 = attention_colscore(q, k, lse, epilogue=_lib.COL_SUM_SQ, causal=True, ref_rounding=ref_rounding,
+                                lse_base2=True)
+    return out, s1, s2
+
+
+def avg_pool1d(x: torch.Tensor, kernel_size: int) -> torch.Tensor:
+    """F.avg_pool1d(x, kernel_size, padding=kernel_size // 2, stride=1) over the last axis of a contiguous fp32
+    [..., n] tensor (snapkv.py:38); kernel_size odd."""
+    dev = _lib.require_gpu(x)
+    if x.dtype != torch.float32 or not x.is_contiguous():
+        raise RuntimeError("avg_pool1d: x must be a contiguous fp32 tensor")
+    n = x.shape[-1]
+    out = torch.empty_like(x)
+    _lib.call("dgg_avg_pool1d", _lib.ptr(x), _lib.ptr(out), x.numel() // n if n else 0, n, int(kernel_size),
+              _lib.stream_handle(dev))
+    return out
+
+
+def snapkv_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, kernel_size: int = 5,
+                     ref_rounding: bool = True):
+    """SnapKV.forward (deepgengraph_exp/cases/kernels/snapkv.py:18-40): causal attention, then the column sums of
+    p pooled by avg_pool1d(kernel_size) along the keys: snapkv_score fp32 [B, Hkv, Sk]. With GQA the per-head sums
+    are averaged over each KV group before the pooling, as h2o_attention does."""
+    out, cs = h2o_attention(q, k, v, ref_rounding=ref_rounding)
+    return out, avg_pool1d(cs.contiguous(), kernel_size)
+
+
+def corm_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, corm_mask: torch.Tensor, *,
+                   ref_rounding: bool = True):
+    """Corm.forward (deepgengraph_exp/cases/kernels/corm.py:18-39): causal attention and
+    corm_score[b, h, j] = any_i p[b, h, i, j] >= corm_mask[i, j] (bool [B, H, Sk]); corm_mask fp32 [Sq, Sk].
+    MHA, as corm.py:16 asserts."""
+    _require_mha("corm_attention", q, k)
+    out, lse = attention(q, k, v, causal=True, return_lse=True, ref_rounding=ref_rounding, lse_base2=True)
+    hit = attention_colscore(q, k, lse, epilogue=_lib.COL_ANY_GE, thr=corm_mask, causal=True,
+                             ref_rounding=ref_rounding, lse_base2=True)
+    return out, hit
+
+
+def kv_gather(k: torch.Tensor, v: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+    """KV-cache compaction after the selection (models/h2o.py:53-57): k / v [B, S, Hkv, D], indices int64
+    [B, Hkv, n] -> kv_cache [B, 2, n, Hkv, D] with kv_cache[b, 0, i, h] = k[b, indices[b, h, i], h] (1: v).
+    Indices outside [0, S) give zero rows."""
+    dev = _lib.require_gpu(k, v, indices)
+    for name, t in (("k", k), ("v", v)):
+        _check_bshd(name, t)
+    if v.shape != k.shape or v.dtype != k.dtype:
+        raise RuntimeError("kv_gather: k and v must match")
+    B, S, Hkv, D = k.shape
+    if indices.dtype != torch.int64 or indices.dim() != 3 or indices.shape[:2] != (B, Hkv) or not indices.is_contiguous():
+        raise RuntimeError(f"kv_gather: indices must be contiguous int64 [{B}, {Hkv}, n]")
+    n = indices.shape[2]
+    out = torch.empty(B, 2, n, Hkv, D, dtype=k.dtype, device=k.device)
+    _lib.call("dgg_kv_gather", _lib.ptr(k), _lib.ptr(v), _lib.ptr(indices), _lib.ptr(out), B, S, Hkv, D, n,
+              _lib.int64_array([*k.stride()[:3], *v.stride()[:3]]), _lib.dtype_code(k.dtype), _lib.stream_handle(dev))
+    return out
+
+
 def topk_indices(scores: torch.Tensor, k: int) -> torch.Tensor:
     """deepgengraph_exp/cases/models/h2o.py:51-52 (torch.topk then sort of the indices) with a defined tie
     order: the k largest of each row of scores [..., n] (fp32), ties broken by the lowest index, returned as int64

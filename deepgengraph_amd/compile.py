@@ -1,10 +1,11 @@
 """The reference's system dispatcher with an MI355X system.
 
 compile(model, input_names, inputs, output_names, system) -> f(*inputs) keeps the signature and contract of the
-reference's compile.py:6-296: `model` is one of the attention case modules (Attn, Gemma2, H2O from
-deepgengraph_exp/cases/kernels/), `f` takes the same positional inputs (q, k, v in [B, S, H, D]) and returns what
-the module's forward returns (out, or (out, h2o_score) for H2O). run_kernel.py:72 and run_e2e.py:217 call it
-this way.
+reference's compile.py:6-296: `model` is one of the attention case modules (Attn, Gemma2, H2O, RoCo, SnapKV, Corm
+from deepgengraph_exp/cases/kernels/), `f` takes the same positional inputs (q, k, v in [B, S, H, D], plus
+corm_mask for Corm) and returns what the module's forward returns (out; (out, h2o_score) for H2O;
+(out, roco_score, roco_sq_score) for RoCo; (out, snapkv_score) for SnapKV; (out, corm_score) for Corm).
+run_kernel.py:72 and run_e2e.py:217 call it this way.
 
 Systems:
   'torch'           the module itself (compile.py:7-8)
@@ -39,8 +40,24 @@ def _attn_f(model):
         def f(q, k, v):
             out, score = _attn.h2o_attention(q, k, v, ref_rounding=True)
             return out, score.view(q.shape[0], int(model.kv_head_num), k.shape[1])
+    elif name == "RoCo":  # roco.py:18-48
+        def f(q, k, v):
+            out, s1, s2 = _attn.roco_attention(q, k, v, ref_rounding=True)
+            shp = (q.shape[0], int(model.kv_head_num), k.shape[1])
+            return out, s1.view(shp), s2.view(shp)
+    elif name == "SnapKV":  # snapkv.py:18-40
+        ks = int(getattr(model, "kernel_size", 5))
+
+        def f(q, k, v):
+            out, score = _attn.snapkv_attention(q, k, v, kernel_size=ks, ref_rounding=True)
+            return out, score.view(q.shape[0], int(model.kv_head_num), k.shape[1])
+    elif name == "Corm":  # corm.py:18-39
+        def f(q, k, v, corm_mask):
+            out, hit = _attn.corm_attention(q, k, v, corm_mask, ref_rounding=True)
+            return out, hit.view(q.shape[0], int(model.kv_head_num), k.shape[1])
     else:
-        raise NotImplementedError(f"system mi355x has no kernel for case {name!r} (supported: Attn, Gemma2, H2O)")
+        raise NotImplementedError(f"system mi355x has no kernel for case {name!r} "
+                                  "(supported: Attn, Gemma2, H2O, RoCo, SnapKV, Corm)")
     return f
 
 

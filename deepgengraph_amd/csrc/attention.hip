@@ -35,6 +35,10 @@ struct AttnParams {
   void* o;
   float* lse;
   float* colsum;
+  float* colsum2;        // column sums of p^2 (kColSumSq)
+  const float* thr;      // [Sq, Sk] thresholds, row stride thr_rs (kColAnyGe)
+  int64_t thr_rs;
+  uint8_t* any_out;      // [B, Hq, Sk] (kColAnyGe)
   int64_t q_sb, q_ss, q_sh;
   int64_t k_sb, k_ss, k_sh;
   int64_t v_sb, v_ss, v_sh;
@@ -124,6 +128,38 @@ template <bool SOFTCAP, bool REFROUND>
 __device__ __forceinline__ float score_coeff(const AttnParams& p) {
   return (SOFTCAP || REFROUND) ? 1.0f : p.c_fast;
 }
+
+// Column epilogues of the column-sum kernels: H2O / SnapKV sum p (h2o.py:35-36, snapkv.py:36-37), RoCo also sums
+// p^2 (roco.py:43-47), Corm ORs p >= threshold[i][j] over the queries (corm.py:35-37).
+enum ColEpi { kColSum = 0, kColSumSq = 1, kColAnyGe = 2 };
+template <int EPI>
+struct ColAcc {
+  float s = 0.f, s2 = 0.f;
+  int any = 0;
+  // p of (query row qi, this lane's key kj); valid = qi < Sq (rows past the end take no part)
+  __device__ __forceinline__ void add(float pe, bool valid, int qi, int kjc, const AttnParams& p) {
+    if constexpr (EPI == kColAnyGe) {
+      if (valid) any |= pe >= p.thr[(int64_t)qi * p.thr_rs + kjc];
+    } else {
+      s += pe;
+      if constexpr (EPI == kColSumSq) s2 = fmaf(pe, pe, s2);
+    }
+  }
+  // Combines the two lane halves (rows 4g..) and stores column kj of (batch, head) bh.
+  __device__ __forceinline__ void store(const AttnParams& p, int bh, int kj, int g) {
+    if constexpr (EPI == kColAnyGe) {
+      const int a = any | __shfl_xor(any, 32, 64);
+      if (g == 0 && kj < p.Sk) p.any_out[(int64_t)bh * p.Sk + kj] = (uint8_t)(a != 0);
+    } else {
+      s += __shfl_xor(s, 32, 64);
+      if constexpr (EPI == kColSumSq) s2 += __shfl_xor(s2, 32, 64);
+      if (g == 0 && kj < p.Sk) {
+        p.colsum[(int64_t)bh * p.Sk + kj] = s;
+        if constexpr (EPI == kColSumSq) p.colsum2[(int64_t)bh * p.Sk + kj] = s2;
+      }
+    }
+  }
+};
 
 // Reference-rounded fp16 scores of two raw fp32 dot products, kept packed (natural-log domain): the matmul
 // output rounded to fp16, divided by ref_div, rounded again (attn.py:29 / h2o.py:29). The conversions are
@@ -757,7 +793,7 @@ attn_fwd_dma_kernel(AttnParams p) {
 constexpr int kCBQ = 64;   // query rows per tile
 constexpr int kCBK = 32 * kWaves;  // keys per workgroup
 
-template <typename T, int D, bool MASK, bool SOFTCAP, bool REFROUND>
+template <typename T, int D, bool MASK, bool SOFTCAP, bool REFROUND, int EPI>
 __global__ void __launch_bounds__(kThreads) attn_colsum_kernel(AttnParams p) {
   typedef typename T::scalar S;
   typedef typename T::vec8 V8;
@@ -837,7 +873,8 @@ __global__ void __launch_bounds__(kThreads) attn_colsum_kernel(AttnParams p) {
   }
   __syncthreads();
 
-  float col = 0.f;
+  ColAcc<EPI> acc;
+  const int kjc = min(kj, p.Sk - 1);
   for (int t = t_begin; t < t_end; ++t) {
     const int buf = (t - t_begin) & 1;
     const bool has_next = t + 1 < t_end;
@@ -868,8 +905,8 @@ __global__ void __launch_bounds__(kThreads) attn_colsum_kernel(AttnParams p) {
         const int row = mb * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
         const float x = score_value<T, SOFTCAP, REFROUND>(sacc[mb][j], p);
         float pe = fast_exp2(fmaf(x, c, -Ls[buf][row]));
+        const int qg = qb + row;
         if (need_mask) {
-          const int qg = qb + row;
           bool ok = qg < p.Sq && kj < p.Sk;
           if constexpr (MASK) {
             const int rel = qg + p.offset - kj;
@@ -878,15 +915,14 @@ __global__ void __launch_bounds__(kThreads) attn_colsum_kernel(AttnParams p) {
           }
           pe = ok ? pe : 0.f;
         }
-        col += pe;
+        acc.add(pe, qg < p.Sq, min(qg, p.Sq - 1), kjc, p);
       }
     }
 
     if (has_next) store_tile(buf ^ 1);
     __syncthreads();
   }
-  col += __shfl_xor(col, 32, 64);
-  if (g == 0 && kj < p.Sk) p.colsum[(int64_t)bh * p.Sk + kj] = col;
+  acc.store(p, bh, kj, g);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -904,7 +940,7 @@ __device__ __forceinline__ void dma4(uint32_t lds, const void* vaddr) {
                : "memory", "m0");
 }
 
-template <typename T, int NW, int BQ, int NSTAGE, bool MASK, bool SOFTCAP, bool REFROUND, bool LSE2>
+template <typename T, int NW, int BQ, int NSTAGE, bool MASK, bool SOFTCAP, bool REFROUND, bool LSE2, int EPI>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_colsum_d128_kernel(AttnParams p) {
   constexpr int D = 128;
@@ -1015,7 +1051,8 @@ attn_colsum_d128_kernel(AttnParams p) {
 
   constexpr bool PK = REFROUND && !SOFTCAP && std::is_same<T, F16>::value;
   const float c = PK ? kLog2e : score_coeff<SOFTCAP, REFROUND>(p);
-  float col = 0.f;
+  ColAcc<EPI> acc;
+  const int kjc = min(kj, p.Sk - 1);
 
   auto tile = [&](const int t, auto masked) {
     const uint32_t st = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B);
@@ -1050,16 +1087,18 @@ attn_colsum_d128_kernel(AttnParams p) {
         else x = score_value<T, SOFTCAP, REFROUND>(sacc[mb][j], p);
         const float l2 = LSE2 ? lv[j >> 2][j & 3] : lv[j >> 2][j & 3] * kLog2e;
         float pe = fast_exp2(fmaf(x, c, -l2));
+        const int o = 32 * mb + 8 * (j >> 2) + (j & 3);
+        bool valid = true;
         if constexpr (decltype(masked)::value) {
-          const int o = 32 * mb + 8 * (j >> 2) + (j & 3);
-          bool ok = o < rows_left;
+          valid = o < rows_left;
+          bool ok = valid;
           if constexpr (MASK) {
             if (p.causal) ok = ok && rel0 + o >= 0;
             if (p.window > 0) ok = ok && rel0 + o < p.window;
           }
           pe = ok ? pe : 0.f;
         }
-        col += pe;
+        acc.add(pe, valid, min(t * BQ + 4 * g + o, p.Sq - 1), kjc, p);
       }
     }
   };
@@ -1087,8 +1126,7 @@ attn_colsum_d128_kernel(AttnParams p) {
   for (int t = t_full0; t < t_full1; ++t) step(t, std::false_type{});
   for (int t = t_full1; t < t_end; ++t) step(t, std::true_type{});
 
-  col += __shfl_xor(col, 32, 64);
-  if (g == 0 && kj < p.Sk) p.colsum[(int64_t)bh * p.Sk + kj] = col;
+  acc.store(p, bh, kj, g);
 }
 
 template <typename T, int D, int BN, bool MASK, bool SOFTCAP, bool REFROUND>
@@ -1097,10 +1135,10 @@ void launch_fwd(const AttnParams& p, hipStream_t st) {
   hipLaunchKernelGGL((attn_fwd_kernel<T, D, BN, MASK, SOFTCAP, REFROUND>), dim3(grid), dim3(kThreads), 0, st, p);
 }
 
-template <typename T, int D, bool MASK, bool SOFTCAP, bool REFROUND>
+template <typename T, int D, bool MASK, bool SOFTCAP, bool REFROUND, int EPI>
 void launch_colsum(const AttnParams& p, hipStream_t st) {
   const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
-  hipLaunchKernelGGL((attn_colsum_kernel<T, D, MASK, SOFTCAP, REFROUND>), dim3(grid), dim3(kThreads), 0, st, p);
+  hipLaunchKernelGGL((attn_colsum_kernel<T, D, MASK, SOFTCAP, REFROUND, EPI>), dim3(grid), dim3(kThreads), 0, st, p);
 }
 
 // head_dim 128 configuration (measured on MI355X, config 2): 8 waves x 32 rows, 128-key tiles, 2-stage ring.
@@ -1158,29 +1196,38 @@ void pick_fwd(const AttnParams& p, bool ref, hipStream_t st) {
 constexpr int kC128NW = 8, kC128BQ = 128, kC128NS = 2;
 constexpr int kC128BK = 32 * kC128NW;  // keys per workgroup (head_dim 128)
 
-template <typename T, bool MASK, bool SOFTCAP, bool REFROUND>
+template <typename T, bool MASK, bool SOFTCAP, bool REFROUND, int EPI>
 void launch_colsum_d128(const AttnParams& p, hipStream_t st) {
   const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
   if (p.lse_base2)
-    hipLaunchKernelGGL((attn_colsum_d128_kernel<T, kC128NW, kC128BQ, kC128NS, MASK, SOFTCAP, REFROUND, true>),
+    hipLaunchKernelGGL((attn_colsum_d128_kernel<T, kC128NW, kC128BQ, kC128NS, MASK, SOFTCAP, REFROUND, true, EPI>),
                        dim3(grid), dim3(64 * kC128NW), 0, st, p);
   else
-    hipLaunchKernelGGL((attn_colsum_d128_kernel<T, kC128NW, kC128BQ, kC128NS, MASK, SOFTCAP, REFROUND, false>),
+    hipLaunchKernelGGL((attn_colsum_d128_kernel<T, kC128NW, kC128BQ, kC128NS, MASK, SOFTCAP, REFROUND, false, EPI>),
                        dim3(grid), dim3(64 * kC128NW), 0, st, p);
 }
 
+template <typename T, int D, bool MASK, bool SOFTCAP, bool REFROUND, int EPI>
+void launch_col(const AttnParams& p, hipStream_t st) {
+  if constexpr (D == 128) launch_colsum_d128<T, MASK, SOFTCAP, REFROUND, EPI>(p, st);
+  else launch_colsum<T, D, MASK, SOFTCAP, REFROUND, EPI>(p, st);
+}
 template <typename T, int D, bool MASK, bool SOFTCAP>
 void pick_col_ref(const AttnParams& p, bool ref, hipStream_t st) {
-  if constexpr (D == 128) {
-    if (ref) launch_colsum_d128<T, MASK, SOFTCAP, true>(p, st);
-    else launch_colsum_d128<T, MASK, SOFTCAP, false>(p, st);
-  } else {
-    if (ref) launch_colsum<T, D, MASK, SOFTCAP, true>(p, st);
-    else launch_colsum<T, D, MASK, SOFTCAP, false>(p, st);
-  }
+  if (ref) launch_col<T, D, MASK, SOFTCAP, true, kColSum>(p, st);
+  else launch_col<T, D, MASK, SOFTCAP, false, kColSum>(p, st);
+}
+// The RoCo / Corm epilogues exist for the mask-checking, soft-cap-free variants only (the reference cases are
+// causal and have no soft-cap); the host rejects a soft-cap with them.
+template <typename T, int D, int EPI>
+void pick_col_epi(const AttnParams& p, bool ref, hipStream_t st) {
+  if (ref) launch_col<T, D, true, false, true, EPI>(p, st);
+  else launch_col<T, D, true, false, false, EPI>(p, st);
 }
 template <typename T, int D>
-void pick_col(const AttnParams& p, bool ref, hipStream_t st) {
+void pick_col(const AttnParams& p, bool ref, int epi, hipStream_t st) {
+  if (epi == kColSumSq) return pick_col_epi<T, D, kColSumSq>(p, ref, st);
+  if (epi == kColAnyGe) return pick_col_epi<T, D, kColAnyGe>(p, ref, st);
   const bool mask = p.causal || p.window > 0;
   const bool sc = p.softcap > 0.f;
   if (mask) {
@@ -1286,17 +1333,33 @@ extern "C" int dgg_attn_prefill(const void* q, const void* k, const void* v, voi
   return dgg::check_launch("attn_prefill");
 }
 
-extern "C" int dgg_attn_colsum(const void* q, const void* k, const float* lse, float* colsum, int64_t B, int64_t Sq,
-                               int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides, float scale,
-                               float softcap, int64_t window, uint32_t flags, int dtype, void* stream) {
-  if (int rc = validate_attn("attn_colsum", q, k, B, Sq, Sk, Hq, Hkv, D, strides, 6, scale, softcap, window, dtype))
-    return rc;
+namespace {
+// Shared body of dgg_attn_colsum and dgg_attn_colscore.
+int colscore(const char* op, const void* q, const void* k, const float* lse, int epi, float* out0, float* out1,
+             uint8_t* out_any, const float* thr, int64_t thr_row_stride, int64_t B, int64_t Sq, int64_t Sk, int64_t Hq,
+             int64_t Hkv, int64_t D, const int64_t* strides, float scale, float softcap, int64_t window, uint32_t flags,
+             int dtype, void* stream) {
+  if (int rc = validate_attn(op, q, k, B, Sq, Sk, Hq, Hkv, D, strides, 6, scale, softcap, window, dtype)) return rc;
+  DGG_REQUIRE(epi == kColSum || epi == kColSumSq || epi == kColAnyGe, DGG_ERR_UNSUPPORTED, "%s: unknown epilogue %d", op,
+              epi);
+  DGG_REQUIRE(epi == kColSum || softcap == 0.f, DGG_ERR_UNSUPPORTED, "%s: epilogue %d takes no soft-cap", op, epi);
   if (B == 0 || Sk == 0) return DGG_OK;
-  DGG_REQUIRE(colsum != nullptr, DGG_ERR_NULL, "attn_colsum: null colsum pointer");
-  DGG_REQUIRE(Sq == 0 || lse != nullptr, DGG_ERR_NULL, "attn_colsum: null lse pointer");
+  if (epi == kColAnyGe) {
+    DGG_REQUIRE(out_any != nullptr, DGG_ERR_NULL, "%s: null output pointer", op);
+    DGG_REQUIRE(Sq == 0 || thr != nullptr, DGG_ERR_NULL, "%s: null threshold pointer", op);
+    DGG_REQUIRE(Sq == 0 || (thr_row_stride >= Sk && thr_row_stride < (1ll << 40)), DGG_ERR_STRIDE,
+                "%s: threshold row stride %lld must be >= Sk (%lld)", op, (long long)thr_row_stride, (long long)Sk);
+  } else {
+    DGG_REQUIRE(out0 != nullptr && (epi != kColSumSq || out1 != nullptr), DGG_ERR_NULL, "%s: null output pointer", op);
+  }
+  DGG_REQUIRE(Sq == 0 || lse != nullptr, DGG_ERR_NULL, "%s: null lse pointer", op);
   AttnParams p = make_params(q, k, nullptr, nullptr, B, Sq, Sk, Hq, Hkv, scale, softcap, window, flags);
   p.lse = const_cast<float*>(lse);
-  p.colsum = colsum;
+  p.colsum = out0;
+  p.colsum2 = out1;
+  p.any_out = out_any;
+  p.thr = thr;
+  p.thr_rs = thr_row_stride;
   p.q_sb = strides[0]; p.q_ss = strides[1]; p.q_sh = strides[2];
   p.k_sb = strides[3]; p.k_ss = strides[4]; p.k_sh = strides[5];
   const int64_t bk = D == 128 ? kC128BK : kCBK;
@@ -1304,13 +1367,29 @@ extern "C" int dgg_attn_colsum(const void* q, const void* k, const float* lse, f
   const bool ref = (flags & DGG_ATTN_REF_ROUNDING) != 0;
   hipStream_t st = dgg::as_stream(stream);
   if (dtype == DGG_BF16) {
-    if (D == 64) pick_col<BF16, 64>(p, ref, st);
-    else if (D == 128) pick_col<BF16, 128>(p, ref, st);
-    else pick_col<BF16, 256>(p, ref, st);
+    if (D == 64) pick_col<BF16, 64>(p, ref, epi, st);
+    else if (D == 128) pick_col<BF16, 128>(p, ref, epi, st);
+    else pick_col<BF16, 256>(p, ref, epi, st);
   } else {
-    if (D == 64) pick_col<F16, 64>(p, ref, st);
-    else if (D == 128) pick_col<F16, 128>(p, ref, st);
-    else pick_col<F16, 256>(p, ref, st);
+    if (D == 64) pick_col<F16, 64>(p, ref, epi, st);
+    else if (D == 128) pick_col<F16, 128>(p, ref, epi, st);
+    else pick_col<F16, 256>(p, ref, epi, st);
   }
-  return dgg::check_launch("attn_colsum");
+  return dgg::check_launch(op);
+}
+}  // namespace
+
+extern "C" int dgg_attn_colsum(const void* q, const void* k, const float* lse, float* colsum, int64_t B, int64_t Sq,
+                               int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides, float scale,
+                               float softcap, int64_t window, uint32_t flags, int dtype, void* stream) {
+  return colscore("attn_colsum", q, k, lse, kColSum, colsum, nullptr, nullptr, nullptr, 0, B, Sq, Sk, Hq, Hkv, D, strides,
+                  scale, softcap, window, flags, dtype, stream);
+}
+
+extern "C" int dgg_attn_colscore(const void* q, const void* k, const float* lse, int epilogue, float* out0, float* out1,
+                                 uint8_t* out_any, const float* thr, int64_t thr_row_stride, int64_t B, int64_t Sq,
+                                 int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides, float scale,
+                                 float softcap, int64_t window, uint32_t flags, int dtype, void* stream) {
+  return colscore("attn_colscore", q, k, lse, epilogue, out0, out1, out_any, thr, thr_row_stride, B, Sq, Sk, Hq, Hkv,
+                  D, strides, scale, softcap, window, flags, dtype, stream);
 }

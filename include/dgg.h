@@ -112,6 +112,35 @@ int dgg_attn_colsum(const void* q, const void* k, const float* lse, float* colsu
                     int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides, float scale,
                     float softcap, int64_t window, uint32_t flags, int dtype, void* stream);
 
+/* Column-score epilogues of dgg_attn_colscore: the other KV-selection cases of the reference on the same
+ * two-pass scheme (forward with lse, then column pass).
+ *   DGG_COL_SUM:    out0[b,h,j] = sum_i p[b,h,i,j]                  (H2O h2o.py:35-36; SnapKV snapkv.py:36-37)
+ *   DGG_COL_SUM_SQ: out0 = sum_i p, out1 = sum_i p^2                (RoCo roco.py:43-47)
+ *   DGG_COL_ANY_GE: out_any[b,h,j] = any_i (p[b,h,i,j] >= thr[i*thr_row_stride + j]), uint8 0/1
+ *                                                                   (Corm corm.py:35-37; thr = corm_mask [Sq, Sk])
+ * Rows i >= Sq take no part; masked pairs have p = 0 (as the reference's softmax of -inf). The two new
+ * epilogues take no soft-cap (DGG_ERR_UNSUPPORTED). Other arguments as dgg_attn_colsum. */
+#define DGG_COL_SUM 0
+#define DGG_COL_SUM_SQ 1
+#define DGG_COL_ANY_GE 2
+int dgg_attn_colscore(const void* q, const void* k, const float* lse, int epilogue, float* out0, float* out1,
+                      uint8_t* out_any, const float* thr, int64_t thr_row_stride, int64_t B, int64_t Sq, int64_t Sk,
+                      int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides, float scale, float softcap,
+                      int64_t window, uint32_t flags, int dtype, void* stream);
+
+/* SnapKV pooling of the column sums (snapkv.py:38: F.avg_pool1d(kernel_size, padding = kernel_size // 2,
+ * stride 1, count_include_pad)): out[r][j] = sum_{|t| <= kernel_size/2} in[r][j+t] / kernel_size with zeros
+ * outside [0, n). in / out fp32 [rows, n] contiguous, not aliased; kernel_size odd. */
+int dgg_avg_pool1d(const float* in, float* out, int64_t rows, int64_t n, int64_t kernel_size, void* stream);
+
+/* KV-cache compaction after top-k (models/h2o.py:53-57, models/snapkv.py:54-57, models/kf.py:57-60):
+ * out [B, 2, n_sel, Hkv, D] contiguous, out[b][0][i][h] = k[b][indices[b][h][i]][h], out[b][1][i][h] = v[...].
+ * k / v are [B, S, Hkv, D] with element strides {batch, seq, head} (k then v: 6 int64); indices int64
+ * [B, Hkv, n_sel] contiguous. An index outside [0, S) yields a zero row (nothing is read out of bounds).
+ * Any dtype; rows of D elements must be a multiple of 16 bytes and 16-byte aligned. */
+int dgg_kv_gather(const void* k, const void* v, const int64_t* indices, void* out, int64_t B, int64_t S, int64_t Hkv,
+                  int64_t D, int64_t n_sel, const int64_t* strides, int dtype, void* stream);
+
 /* Top-k of H2O scores (deepgengraph_exp/cases/models/h2o.py:51-52: torch.topk then sort of the indices):
  * for each of `rows` rows of n fp32 scores (row stride n), the k largest, ties broken by the lowest index,
  * written as int64 indices in ascending index order to out_idx [rows, k]. -0.0 equals +0.0; NaN is not

@@ -104,6 +104,82 @@ def h2o(q, k, v, *, q_chunk=256):
     return out.transpose(1, 2).contiguous(), colsum, lse
 
 
+def _causal_probs(q, k, v, q_chunk):
+    """Shared body of the KV-selection cases (roco.py / snapkv.py / corm.py: MHA, causal, `scores += mask`,
+    fp32 softmax, out = probs.to(dtype) @ v). Yields (i0, n, probs [B, H, n, Sk] fp32) per query chunk and fills
+    out [B, H, Sq, D] and lse [B, H, Sq] in place; returns (out, lse) holders."""
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    assert k.shape[2] == H, "the reference's selection cases are multi-head attention (roco.py:16 etc.)"
+    dt = q.dtype
+    qt, kt, vt = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    kT = kt.transpose(-2, -1)
+    out = torch.empty(B, H, Sq, D, dtype=dt)
+    lse = torch.empty(B, H, Sq, dtype=torch.float32)
+
+    def gen():
+        for i0 in range(0, Sq, q_chunk):
+            n = min(q_chunk, Sq - i0)
+            scores = torch.matmul(qt[:, :, i0:i0 + n], kT) / math.sqrt(D)  # roco.py:37 / snapkv.py:31 / corm.py:30
+            scores = scores.masked_fill(_mask(i0, n, Sq, Sk, True, None), float("-inf"))
+            sf = scores.float()
+            probs = torch.softmax(sf, dim=-1)
+            out[:, :, i0:i0 + n] = torch.matmul(probs.to(dt), vt)
+            lse[:, :, i0:i0 + n] = torch.logsumexp(sf, dim=-1)
+            yield i0, n, probs
+
+    return gen(), out, lse
+
+
+def roco(q, k, v, *, q_chunk=256):
+    """RoCo.forward (deepgengraph_exp/cases/kernels/roco.py:18-48): causal attention plus the fp32 column sums of
+    p and of p^2 over the query axis (roco.py:43-47). Returns (out, roco_score, roco_sq_score, lse)."""
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    rows, out, lse = _causal_probs(q, k, v, q_chunk)
+    s1 = torch.zeros(B, H, Sk, dtype=torch.float32)
+    s2 = torch.zeros(B, H, Sk, dtype=torch.float32)
+    for _, _, probs in rows:
+        s1 += probs.sum(dim=2)           # roco.py:43, 46
+        s2 += (probs ** 2).sum(dim=2)    # roco.py:44, 47
+    return out.transpose(1, 2).contiguous(), s1, s2, lse
+
+
+def snapkv(q, k, v, *, kernel_size=5, q_chunk=256):
+    """SnapKV.forward (deepgengraph_exp/cases/kernels/snapkv.py:18-40): causal attention plus the column sums
+    (snapkv.py:36-37) smoothed by F.avg_pool1d(kernel_size, padding=kernel_size // 2, stride=1) (snapkv.py:38).
+    Returns (out, snapkv_score, lse)."""
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    rows, out, lse = _causal_probs(q, k, v, q_chunk)
+    cs = torch.zeros(B, H, Sk, dtype=torch.float32)
+    for _, _, probs in rows:
+        cs += probs.sum(dim=2)
+    pooled = torch.nn.functional.avg_pool1d(cs, kernel_size=kernel_size, padding=kernel_size // 2, stride=1)
+    return out.transpose(1, 2).contiguous(), pooled, lse
+
+
+def corm(q, k, v, corm_mask, *, q_chunk=256):
+    """Corm.forward (deepgengraph_exp/cases/kernels/corm.py:18-39): causal attention plus
+    corm_score[b, h, j] = any_i (probs[b, h, i, j] >= corm_mask[i, j]) (corm.py:35-37), a bool [B, H, Sk].
+    corm_mask is fp32 [Sq, Sk] (corm.py:47-49 builds 1 / (i + 1)). Returns (out, corm_score, lse)."""
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    rows, out, lse = _causal_probs(q, k, v, q_chunk)
+    hit = torch.zeros(B, H, Sk, dtype=torch.bool)
+    for i0, n, probs in rows:
+        hit |= (probs >= corm_mask[i0:i0 + n]).any(dim=2)
+    return out.transpose(1, 2).contiguous(), hit, lse
+
+
+def corm_mask(q_len: int, kv_len: int) -> torch.Tensor:
+    """Corm.prepare's threshold (corm.py:47-49): row i of ones divided by i + 1, fp32 [q_len, kv_len]."""
+    m = torch.ones(q_len, kv_len, dtype=torch.float32)
+    for i in range(q_len):
+        m[i] /= i + 1
+    return m
+
+
 def decode(q, k_cache, v_cache):
     """Attn.forward with q_len == 1 (attn.py:18-34): the mask triu(diagonal = L) hides nothing (attn.py:22-23).
 

@@ -68,6 +68,40 @@ def colsum(q, k, *, causal=True, scale=None):
     return cs
 
 
+def colscores(q, k, *, thr=None):
+    """Causal MHA column scores in float64 loops: (sum_i p, sum_i p^2, any_i p >= thr[i][j]) per (b, h, j)
+    (roco.py:43-47, corm.py:35-37; masked pairs have p = 0)."""
+    B, Sq, H, D = len(q), len(q[0]), len(q[0][0]), len(q[0][0][0])
+    Sk = len(k[0])
+    scale = 1.0 / math.sqrt(D)
+    off = Sk - Sq
+    s1 = [[[0.0] * Sk for _ in range(H)] for _ in range(B)]
+    s2 = [[[0.0] * Sk for _ in range(H)] for _ in range(B)]
+    hit = [[[False] * Sk for _ in range(H)] for _ in range(B)]
+    for b in range(B):
+        for h in range(H):
+            for i in range(Sq):
+                xs = {j: sum(float(q[b][i][h][d]) * float(k[b][j][h][d]) for d in range(D)) * scale
+                      for j in range(Sk) if j <= i + off}
+                if not xs:
+                    continue
+                m = max(xs.values())
+                den = sum(math.exp(s - m) for s in xs.values())
+                for j in range(Sk):
+                    pr = math.exp(xs[j] - m) / den if j in xs else 0.0
+                    s1[b][h][j] += pr
+                    s2[b][h][j] += pr * pr
+                    if thr is not None and pr >= float(thr[i][j]):
+                        hit[b][h][j] = True
+    return s1, s2, hit
+
+
+def avg_pool(row, ks):
+    """Mean over the window [j - ks//2, j + ks//2] of a list, zeros outside, divided by ks."""
+    n, h = len(row), ks // 2
+    return [sum(row[t] for t in range(j - h, j + h + 1) if 0 <= t < n) / ks for j in range(n)]
+
+
 def rms_norm(x, w, eps):
     """Rows of x: y_i = x_i / sqrt(mean(x^2) + eps) * w_i (csrc/norm.cu:34-56 without rounding)."""
     out = []

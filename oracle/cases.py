@@ -1,6 +1,7 @@
 """The reference's attention case modules restated on the CPU oracle — TEST INFRASTRUCTURE ONLY.
 
-Same class names, constructor arguments and attributes as deepgengraph_exp/cases/kernels/{attn,gemma2,h2o}.py,
+Same class names, constructor arguments and attributes as deepgengraph_exp/cases/kernels/{attn,gemma2,h2o,roco,
+snapkv,corm}.py,
 so that tests can hand them to deepgengraph_amd.compile.compile() exactly as run_kernel.py:44-78 does. forward()
 evaluates the oracle (oracle/attention.py) on CPU copies of the inputs and returns CPU tensors.
 """
@@ -60,3 +61,39 @@ class H2O(_Case):
     def forward(self, q, k, v):
         out, colsum, _ = _oa.h2o(q.cpu(), k.cpu(), v.cpu())
         return out, colsum.view(q.shape[0], self.kv_head_num, k.shape[1])
+
+
+class RoCo(_Case):
+    """deepgengraph_exp/cases/kernels/roco.py:7-48."""
+    OUTPUTS = ("out", "roco_score", "roco_sq_score")
+
+    def forward(self, q, k, v):
+        out, s1, s2, _ = _oa.roco(q.cpu(), k.cpu(), v.cpu())
+        return out, s1, s2
+
+
+class SnapKV(_Case):
+    """deepgengraph_exp/cases/kernels/snapkv.py:7-40."""
+    OUTPUTS = ("out", "snapkv_score")
+
+    def __init__(self, kernel_size=5, kv_head_num=32, head_num=32, head_dim=128):
+        super().__init__(kv_head_num, head_num, head_dim)
+        self.kernel_size = kernel_size
+
+    def forward(self, q, k, v):
+        out, score, _ = _oa.snapkv(q.cpu(), k.cpu(), v.cpu(), kernel_size=self.kernel_size)
+        return out, score
+
+
+class Corm(_Case):
+    """deepgengraph_exp/cases/kernels/corm.py:7-58 (prepare adds corm_mask = 1 / (i + 1), corm.py:47-49)."""
+    OUTPUTS = ("out", "corm_score")
+
+    def prepare(self, batch_size=1, q_len=4096, kv_len=4096, dtype=torch.float16, device="cpu", seed=0):
+        spec = super().prepare(batch_size, q_len, kv_len, dtype, device, seed)
+        spec["input"]["corm_mask"] = _oa.corm_mask(q_len, kv_len).to(device)
+        return spec
+
+    def forward(self, q, k, v, corm_mask):
+        out, hit, _ = _oa.corm(q.cpu(), k.cpu(), v.cpu(), corm_mask.cpu())
+        return out, hit

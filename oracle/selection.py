@@ -1,7 +1,9 @@
-"""CPU restatement of the H2O key selection — TEST INFRASTRUCTURE ONLY (see oracle/__init__.py)."""
+"""CPU restatement of the KV-cache selection (top-k, SnapKV pooling, compaction gather) — TEST INFRASTRUCTURE ONLY
+(see oracle/__init__.py)."""
 from __future__ import annotations
 
 import numpy as np
+import torch
 
 
 def topk_indices(scores: np.ndarray, k: int) -> np.ndarray:
@@ -13,3 +15,23 @@ def topk_indices(scores: np.ndarray, k: int) -> np.ndarray:
     s = np.asarray(scores, dtype=np.float32)
     order = np.argsort(-s, axis=-1, kind="stable")[..., :k]
     return np.sort(order, axis=-1).astype(np.int64)
+
+
+def avg_pool1d(x: torch.Tensor, kernel_size: int) -> torch.Tensor:
+    """snapkv.py:38: F.avg_pool1d(x, kernel_size, padding=kernel_size // 2, stride=1) over the last axis of a
+    fp32 [..., n] tensor (zero padding counted in the mean)."""
+    shp = x.shape
+    y = torch.nn.functional.avg_pool1d(x.reshape(-1, 1, shp[-1]), kernel_size=kernel_size, padding=kernel_size // 2,
+                                       stride=1)
+    return y.reshape(*shp[:-1], y.shape[-1])
+
+
+def kv_gather(k: torch.Tensor, v: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+    """models/h2o.py:53-57: k/v [B, S, Hkv, D], indices [B, Hkv, n] (sorted top-k positions) ->
+    kv_cache [B, 2, n, Hkv, D] = cat(gather(k), gather(v)) along a new axis 1."""
+    B, S, Hkv, D = k.shape
+    n = indices.shape[-1]
+    idx = indices.transpose(1, 2)[:, :, :, None].expand(B, n, Hkv, D)  # models/h2o.py:53
+    kc = torch.gather(k, dim=1, index=idx).view(B, 1, n, Hkv, D)     # models/h2o.py:54
+    vc = torch.gather(v, dim=1, index=idx).view(B, 1, n, Hkv, D)     # models/h2o.py:55
+    return torch.cat([kc, vc], dim=1)                                # models/h2o.py:56

@@ -205,3 +205,75 @@ def test_topk_selection():
         row = rng.integers(0, 4, size=40).astype(np.float32)
         k = int(rng.integers(1, 40))
         np.testing.assert_array_equal(osel.topk_indices(row[None], k)[0], brute.topk_indices(row.tolist(), k))
+
+
+def _sel_inputs(seed, B=1, S=20, H=2, D=8, Sk=None, scale=2.0):
+    g = torch.Generator().manual_seed(seed)
+    Sk = S if Sk is None else Sk
+    q = torch.randn(B, S, H, D, generator=g) * scale
+    k = torch.randn(B, Sk, H, D, generator=g)
+    v = torch.randn(B, Sk, H, D, generator=g)
+    return q, k, v
+
+
+def test_roco_matches_brute_and_invariants():
+    q, k, v = _sel_inputs(5)
+    out, s1, s2, lse = oa.roco(q, k, v)
+    b1, b2, _ = brute.colscores(q.tolist(), k.tolist())
+    assert_close(s1, torch.tensor(b1), 1e-6, 1e-5, "roco sum vs brute")
+    assert_close(s2, torch.tensor(b2), 1e-6, 1e-5, "roco sum of squares vs brute")
+    # the sum part is the H2O column sum; the last key is seen by the last query only, so s2 = s1^2 there
+    assert_close(s1, oa.h2o(q, k, v)[1], 0, 0, "roco sum == h2o colsum")
+    assert_close(s2[..., -1], s1[..., -1] ** 2, 1e-7, 1e-6, "single-probability column")
+    assert (s2 <= s1 + 1e-7).all() and (s2 > 0).all()
+    assert_close(s1.sum(-1), torch.full((1, 2), 20.0), 0, 1e-5, "sum of column sums = q_len")
+    assert_close(out, oa.attention(q, k, v), 0, 0, "roco out == attention")
+
+
+def test_snapkv_pool_matches_brute_and_closed_form():
+    q, k, v = _sel_inputs(6, S=23)
+    out, pooled, _ = oa.snapkv(q, k, v)
+    cs = oa.h2o(q, k, v)[1]
+    want = torch.tensor([[brute.avg_pool(cs[0, h].tolist(), 5) for h in range(2)]])
+    assert_close(pooled, want, 1e-7, 1e-6, "snapkv pooled vs brute")
+    # a constant row pools to 3/5, 4/5, 1, ..., 1, 4/5, 3/5 (zero padding counted)
+    ones = torch.ones(2, 3, 9)
+    p1 = osel.avg_pool1d(ones, 5)
+    assert_close(p1[0, 0], torch.tensor([0.6, 0.8, 1, 1, 1, 1, 1, 0.8, 0.6]), 1e-7, 1e-6, "pool of ones")
+    x = torch.randn(3, 17)
+    for ks in (1, 3, 7):
+        got = osel.avg_pool1d(x, ks)
+        assert_close(got, torch.tensor([brute.avg_pool(r, ks) for r in x.tolist()]), 1e-6, 1e-6, f"pool k={ks}")
+
+
+def test_corm_matches_brute_and_closed_form():
+    q, k, v = _sel_inputs(7, S=18, scale=1.5)
+    thr = oa.corm_mask(18, 18)
+    out, hit, _ = oa.corm(q, k, v, thr)
+    _, _, bh = brute.colscores(q.tolist(), k.tolist(), thr=thr.tolist())
+    assert hit.dtype == torch.bool and hit.shape == (1, 2, 18)
+    assert torch.equal(hit, torch.tensor(bh)), "corm any(p >= 1/(i+1)) vs brute"
+    # key 0 is the whole row 0 (p = 1 >= 1): always selected
+    assert hit[..., 0].all()
+    # q = 0: every visible p is exactly 1/(i+1), equal to the threshold, so ">=" selects every key (">" would not)
+    out0, hit0, _ = oa.corm(torch.zeros_like(q), k, v, thr)
+    assert hit0.all()
+    assert torch.equal(thr[3], torch.full((18,), 1.0 / 4, dtype=torch.float32))
+
+
+def test_kv_gather_matches_loops():
+    g = torch.Generator().manual_seed(8)
+    B, S, H, D, n = 2, 30, 3, 8, 7
+    k = torch.randn(B, S, H, D, generator=g).half()
+    v = torch.randn(B, S, H, D, generator=g).half()
+    idx = torch.stack([torch.stack([torch.sort(torch.randperm(S, generator=g)[:n])[0] for _ in range(H)])
+                       for _ in range(B)])
+    kv = osel.kv_gather(k, v, idx)
+    assert kv.shape == (B, 2, n, H, D)
+    for b in range(B):
+        for h in range(H):
+            for i in range(n):
+                j = int(idx[b, h, i])
+                assert torch.equal(kv[b, 0, i, h], k[b, j, h]) and torch.equal(kv[b, 1, i, h], v[b, j, h])
+    ident = torch.arange(n).view(1, 1, n).expand(B, H, n).contiguous()
+    assert torch.equal(osel.kv_gather(k, v, ident)[:, 0], k[:, :n])

@@ -63,15 +63,14 @@ attn_fwd_dma_kernel(AttnParams p) {
   const char* vp = reinterpret_cast<const char*>(static_cast<const S*>(p.v) + b * p.v_sb + hk * p.v_sh);
   const int64_t k_ss_b = p.k_ss * (int64_t)sizeof(S), v_ss_b = p.v_ss * (int64_t)sizeof(S);
 
+  // Q fragments: all loads issued back to back (rows past the end read the last row and are zeroed afterwards;
+  // a load under a per-row branch would be waited for on its own).
   V8 qf[NQB][D / 16];
 #pragma unroll
   for (int n = 0; n < NQB; ++n) {
-    const int qi = qw0 + 32 * n + r;
+    const int qi = min(qw0 + 32 * n + r, p.Sq - 1);
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) {
-      if (qi < p.Sq) qf[n][kk] = ld16<V8>(qp + (int64_t)qi * p.q_ss + 16 * kk + 8 * g);
-      else qf[n][kk] = V8{};
-    }
+    for (int kk = 0; kk < D / 16; ++kk) qf[n][kk] = ld16<V8>(qp + (int64_t)qi * p.q_ss + 16 * kk + 8 * g);
   }
   // BIAS (bf16 without soft-cap or reference rounding, no lse): Q is pre-scaled by scale*log2(e) and each score
   // accumulator starts from -m (the row's reference maximum) through one extra MFMA whose A fragment is the
@@ -79,21 +78,23 @@ attn_fwd_dma_kernel(AttnParams p) {
   // P = exp2(acc) needs no per-element arithmetic. The reference maxima are bf16 values so that -m is exact in
   // the B operand; the pre-scaled Q carries the same 2^-9 relative rounding as the reference's bf16 scores.
   constexpr bool BIAS = FASTSUM && !SOFTCAP && !REFROUND && std::is_same<T, BF16>::value;
-  if constexpr (BIAS) {
+  // Waits for the Q loads (after the first K / V copies are issued, so that the latencies overlap), zeroes rows
+  // past the end, pre-scales for BIAS and pins the fragments in registers: AGPRs at one wave per SIMD (head_dim
+  // 256: MFMA reads its B operand from there, the VGPRs stay free for the scores and the fragments read ahead).
+  auto finish_q = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int n = 0; n < NQB; ++n)
+    for (int n = 0; n < NQB; ++n) {
+      const bool live = qw0 + 32 * n + r < p.Sq;
 #pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk) qf[n][kk] = from_f32x8<V8>(to_f32x8(qf[n][kk]) * p.c_fast);
-  }
-#pragma unroll
-  for (int n = 0; n < NQB; ++n)
-#pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) {
-      // At one wave per SIMD (head_dim 256) Q lives in AGPRs (MFMA reads its B operand from there), which
-      // leaves the VGPRs to the S scores and to K / V fragments read ahead of their MFMAs.
-      if constexpr (OCC == 1) asm volatile("" : "+a"(qf[n][kk]));
-      else asm volatile("" : "+v"(qf[n][kk]));
+      for (int kk = 0; kk < D / 16; ++kk) {
+        asm volatile("" : "+v"(qf[n][kk]));
+        if (!live) qf[n][kk] = V8{};
+        if constexpr (BIAS) qf[n][kk] = from_f32x8<V8>(to_f32x8(qf[n][kk]) * p.c_fast);
+        if constexpr (OCC == 1) asm volatile("" : "+a"(qf[n][kk]));
+        else asm volatile("" : "+v"(qf[n][kk]));
+      }
     }
+  };
   V8 abias = V8{};
   abias[0] = g == 0 ? to_s<S>(1.0f) : to_s<S>(0.0f);
   V8 bbias[NQB];
@@ -347,6 +348,7 @@ attn_fwd_dma_kernel(AttnParams p) {
 #pragma unroll
   for (int i = 0; i < NSTAGE - 1; ++i)
     if (t_begin + i < t_end) issue(t_begin + i);
+  finish_q();
   auto step = [&](const int t, auto masked) {
     const int after = min(NSTAGE - 2, t_end - 1 - t);
     if (NSTAGE >= 4 && after >= 2) wait_vmem<2 * DMA_PER_TILE>();
@@ -420,12 +422,13 @@ __global__ void __launch_bounds__(kThreads) attn_colsum_kernel(AttnParams p) {
 
   V8 kf[NKK];
 #pragma unroll
-  for (int kk = 0; kk < NKK; ++kk) {
-    if (kj < p.Sk) kf[kk] = ld16<V8>(kp + (int64_t)kj * p.k_ss + 16 * kk + 8 * g);
-    else kf[kk] = V8{};
-  }
+  for (int kk = 0; kk < NKK; ++kk)  // back-to-back loads (keys past the end read the last key, zeroed below)
+    kf[kk] = ld16<V8>(kp + (int64_t)min(kj, p.Sk - 1) * p.k_ss + 16 * kk + 8 * g);
 #pragma unroll
-  for (int kk = 0; kk < NKK; ++kk) asm volatile("" : "+v"(kf[kk]));  // see the forward kernel
+  for (int kk = 0; kk < NKK; ++kk) {
+    asm volatile("" : "+v"(kf[kk]));  // see the forward kernel
+    if (kj >= p.Sk) kf[kk] = V8{};
+  }
 
   // Query range that can see any key of this tile.
   const int k_last = min(k0 + kCBK, p.Sk) - 1;
@@ -574,12 +577,13 @@ attn_colsum_d128_kernel(AttnParams p) {
 
   V8 kf[D / 16];
 #pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk) {
-    if (kj < p.Sk) kf[kk] = ld16<V8>(kp + (int64_t)kj * p.k_ss + 16 * kk + 8 * g);
-    else kf[kk] = V8{};
-  }
+  for (int kk = 0; kk < D / 16; ++kk)  // back-to-back loads (keys past the end read the last key, zeroed below)
+    kf[kk] = ld16<V8>(kp + (int64_t)min(kj, p.Sk - 1) * p.k_ss + 16 * kk + 8 * g);
 #pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(kf[kk]));  // see the forward kernel
+  for (int kk = 0; kk < D / 16; ++kk) {
+    asm volatile("" : "+v"(kf[kk]));  // see the forward kernel
+    if (kj >= p.Sk) kf[kk] = V8{};
+  }
 
   // Query tiles that see any key of the workgroup, and of this wave.
   const int k_last = min(k0 + BK, p.Sk) - 1;

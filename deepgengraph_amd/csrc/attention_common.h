@@ -215,14 +215,15 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D
   // Q fragment (B operand of S^T = K.Q^T): lane holds query qi, head-dim elements 16kk + 8g .. +8.
   V8 qf[NKK];
 #pragma unroll
-  for (int kk = 0; kk < NKK; ++kk) {
-    if (qi < p.Sq) qf[kk] = ld16<V8>(qp + (int64_t)qi * p.q_ss + 16 * kk + 8 * g);
-    else qf[kk] = V8{};
-  }
+  for (int kk = 0; kk < NKK; ++kk)  // back-to-back loads (rows past the end read the last row, zeroed below)
+    qf[kk] = ld16<V8>(qp + (int64_t)min(qi, p.Sq - 1) * p.q_ss + 16 * kk + 8 * g);
   // Re-define the Q registers here (after their loads complete) so that the main loop's wait counting does not
   // treat them as results of outstanding vector-memory loads.
 #pragma unroll
-  for (int kk = 0; kk < NKK; ++kk) asm volatile("" : "+v"(qf[kk]));
+  for (int kk = 0; kk < NKK; ++kk) {
+    asm volatile("" : "+v"(qf[kk]));
+    if (qi >= p.Sq) qf[kk] = V8{};
+  }
 
   // Key range of this query tile.
   const int q_last = min(q0 + kBM, p.Sq) - 1;

@@ -62,10 +62,13 @@ __global__ void __launch_bounds__(kDecThreads) decode_partial_kernel(DecodeParam
     bool ok[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
+      // Keys past the split's end re-read its last key (finite; masked to p = 0 below), so that all 2*kUnroll
+      // loads go out back to back: a load under a per-lane branch is waited for on its own.
       const int key = base + u * GROUPS + grp;
       ok[u] = key < k1;
-      kr[u] = ok[u] ? ld16<V8>(kp + (int64_t)key * p.k_sl) : V8{};
-      vr[u] = ok[u] ? ld16<V8>(vp + (int64_t)key * p.v_sl) : V8{};
+      const int kc = min(key, k1 - 1);
+      kr[u] = ld16<V8>(kp + (int64_t)kc * p.k_sl);
+      vr[u] = ld16<V8>(vp + (int64_t)kc * p.v_sl);
     }
     float s[kUnroll];
     float bm = -INFINITY;

@@ -204,6 +204,25 @@ attn_fwd_dma_kernel(AttnParams p) {
       asm volatile("" : "+v"(kbase[i]), "+v"(vbase[i]));
     }
     constexpr int NMB = BN / 32;
+    constexpr bool MASKED = decltype(masked)::value;
+    // Masked tiles: per 32-key block, whether any of the wave's rows sees any of its keys (live) and whether every
+    // row sees every key (full). Dead blocks skip their MFMAs and exps, full blocks the per-element mask.
+    bool blk_live[NMB], blk_full[NMB];
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) blk_live[mb] = blk_full[mb] = true;
+    if constexpr (MASKED) {
+      const int row_hi = max(qw0, min(qw0 + QPW, p.Sq) - 1);
+      const int hi_min = p.causal ? min(p.Sk - 1, qw0 + p.offset) : p.Sk - 1;
+      const int hi_max = p.causal ? min(p.Sk - 1, row_hi + p.offset) : p.Sk - 1;
+      const int lo_min = p.window > 0 ? max(0, qw0 + p.offset - p.window + 1) : 0;
+      const int lo_max = p.window > 0 ? max(0, row_hi + p.offset - p.window + 1) : 0;
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb) {
+        const int kb0 = t * BN + mb * 32;
+        blk_live[mb] = kb0 <= hi_max && kb0 + 31 >= lo_min;
+        blk_full[mb] = kb0 >= lo_max && kb0 + 31 <= hi_min;
+      }
+    }
     f32x16 sacc[NQB][NMB];
 #pragma unroll
     for (int n = 0; n < NQB; ++n)
@@ -212,13 +231,26 @@ attn_fwd_dma_kernel(AttnParams p) {
         if constexpr (BIAS) sacc[n][mb] = mfma32(abias, bbias[n], f32x16{});  // every element = -m[n]
         else sacc[n][mb] = f32x16{};
       }
-#pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) {
+    if constexpr (MASKED) {
 #pragma unroll
       for (int mb = 0; mb < NMB; ++mb) {
-        const V8 a = lds_read<V8>(kbase[kk >> 1] + mb * 8 * GROUP_B + 32 * (kk & 1));
+        if (!blk_live[mb]) continue;
 #pragma unroll
-        for (int n = 0; n < NQB; ++n) sacc[n][mb] = mfma32(a, qf[n][kk], sacc[n][mb]);
+        for (int kk = 0; kk < D / 16; ++kk) {
+          const V8 a = lds_read<V8>(kbase[kk >> 1] + mb * 8 * GROUP_B + 32 * (kk & 1));
+#pragma unroll
+          for (int n = 0; n < NQB; ++n) sacc[n][mb] = mfma32(a, qf[n][kk], sacc[n][mb]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk) {
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb) {
+          const V8 a = lds_read<V8>(kbase[kk >> 1] + mb * 8 * GROUP_B + 32 * (kk & 1));
+#pragma unroll
+          for (int n = 0; n < NQB; ++n) sacc[n][mb] = mfma32(a, qf[n][kk], sacc[n][mb]);
+        }
       }
     }
     const int kb4 = t * BN + 4 * g;
@@ -249,9 +281,10 @@ attn_fwd_dma_kernel(AttnParams p) {
             float x;
             if constexpr (PK) x = (float)hs[n][mb][j >> 1][j & 1];
             else x = score_value<T, SOFTCAP, REFROUND>(sacc[n][mb][j], p);
-            if constexpr (decltype(masked)::value) {
+            if constexpr (MASKED) {
               const int o = mb * 32 + 8 * (j >> 2) + (j & 3);
-              x = (o <= rel_hi && o >= rel_lo) ? x : -INFINITY;
+              if (!blk_live[mb]) x = -INFINITY;
+              else if (!blk_full[mb]) x = (o <= rel_hi && o >= rel_lo) ? x : -INFINITY;
             }
             sacc[n][mb][j] = x;
             mloc = fmaxf(mloc, x);
@@ -297,6 +330,7 @@ attn_fwd_dma_kernel(AttnParams p) {
     for (int n = 0; n < NQB; ++n) mcs[n] = BIAS || m_run[n] == -INFINITY ? 0.f : m_run[n] * c;
 #pragma unroll
     for (int kk = 0; kk < BN / 16; ++kk) {
+      if (MASKED && !blk_live[kk >> 1]) continue;  // P = 0 there
       V8 pb[NQB];
 #pragma unroll
       for (int n = 0; n < NQB; ++n) {

@@ -44,6 +44,10 @@ SIGNATURES = {
                                _u32, _i32, _vp]),
     "dgg_attn_colscore": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                  _i64p, _f32, _f32, _i64, _u32, _i32, _vp]),
+    "dgg_attn_kf_rowlse": (_i32, [_vp, _vp, _vp, _i64p, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64p, _f32, _f32,
+                                  _i64, _u32, _i32, _vp]),
+    "dgg_attn_kf_colsum": (_i32, [_vp, _vp, _vp, _i64p, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64p, _f32,
+                                  _f32, _i64, _u32, _i32, _vp]),
     "dgg_avg_pool1d": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp]),
     "dgg_kv_gather": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64p, _i32, _vp]),
     "dgg_topk_indices": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp]),

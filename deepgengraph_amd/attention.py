@@ -178,6 +178,34 @@ def corm_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, corm_mask:
     return out, hit
 
 
+def keyformer_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exp_rand: torch.Tensor, *,
+                        tau: float = 1.5, ref_rounding: bool = True):
+    """KeyFormer.forward (deepgengraph_exp/cases/kernels/kf.py:18-40): causal attention `out` [B, S, H, D] and
+    kf_score [B, H, Sk] fp32, the column sums over the queries of softmax((scores + gumbels) / tau) with
+    gumbels = -log(exp_rand) (kf.py:36-40); exp_rand fp32 [B, H, Sq, Sk] (unit key stride). MHA, as kf.py:16
+    asserts. Three launches: the forward, the perturbed row lse, the column pass."""
+    _require_mha("keyformer_attention", q, k)
+    dev = _lib.require_gpu(q, k, v, exp_rand)
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    if (exp_rand.dtype != torch.float32 or exp_rand.dim() != 4 or tuple(exp_rand.shape) != (B, H, Sq, Sk)
+            or exp_rand.stride(-1) != 1):
+        raise RuntimeError(f"keyformer_attention: exp_rand must be fp32 [{B}, {H}, {Sq}, {Sk}] with unit key stride")
+    out = attention(q, k, v, causal=True, ref_rounding=ref_rounding)
+    scale = 1.0 / math.sqrt(D)
+    flags = _lib.ATTN_CAUSAL | (_lib.ATTN_REF_ROUNDING if ref_rounding else 0)
+    strides = _lib.int64_array([*q.stride()[:3], *k.stride()[:3]])
+    er_strides = _lib.int64_array(list(exp_rand.stride()[:3]))
+    lse2 = torch.empty(B, H, Sq, dtype=torch.float32, device=q.device)
+    _lib.call("dgg_attn_kf_rowlse", _lib.ptr(q), _lib.ptr(k), _lib.ptr(exp_rand), er_strides, _lib.ptr(lse2), B, Sq,
+              Sk, H, H, D, strides, scale, float(tau), 0, flags, _lib.dtype_code(q.dtype), _lib.stream_handle(dev))
+    score = torch.empty(B, H, Sk, dtype=torch.float32, device=q.device)
+    _lib.call("dgg_attn_kf_colsum", _lib.ptr(q), _lib.ptr(k), _lib.ptr(exp_rand), er_strides, _lib.ptr(lse2),
+              _lib.ptr(score), B, Sq, Sk, H, H, D, strides, scale, float(tau), 0, flags, _lib.dtype_code(q.dtype),
+              _lib.stream_handle(dev))
+    return out, score
+
+
 def kv_gather(k: torch.Tensor, v: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
     """KV-cache compaction after the selection (models/h2o.py:53-57): k / v [B, S, Hkv, D], indices int64
     [B, Hkv, n] -> kv_cache [B, 2, n, Hkv, D] with kv_cache[b, 0, i, h] = k[b, indices[b, h, i], h] (1: v).

@@ -1,10 +1,11 @@
 """The reference's system dispatcher with an MI355X system.
 
 compile(model, input_names, inputs, output_names, system) -> f(*inputs) keeps the signature and contract of the
-reference's compile.py:6-296: `model` is one of the attention case modules (Attn, Gemma2, H2O, RoCo, SnapKV, Corm
+reference's compile.py:6-296: `model` is one of the attention case modules (Attn, Gemma2, H2O, RoCo, SnapKV, Corm, KeyFormer
 from deepgengraph_exp/cases/kernels/), `f` takes the same positional inputs (q, k, v in [B, S, H, D], plus
-corm_mask for Corm) and returns what the module's forward returns (out; (out, h2o_score) for H2O;
-(out, roco_score, roco_sq_score) for RoCo; (out, snapkv_score) for SnapKV; (out, corm_score) for Corm).
+corm_mask for Corm and exp_rand for KeyFormer) and returns what the module's forward returns (out; (out, h2o_score)
+for H2O; (out, roco_score, roco_sq_score) for RoCo; (out, snapkv_score) for SnapKV; (out, corm_score) for Corm;
+(out, kf_score) for KeyFormer).
 run_kernel.py:72 and run_e2e.py:217 call it this way.
 
 Systems:
@@ -55,9 +56,15 @@ def _attn_f(model):
         def f(q, k, v, corm_mask):
             out, hit = _attn.corm_attention(q, k, v, corm_mask, ref_rounding=True)
             return out, hit.view(q.shape[0], int(model.kv_head_num), k.shape[1])
+    elif name == "KeyFormer":  # kf.py:18-40
+        tau = float(getattr(model, "tau", 1.5))
+
+        def f(q, k, v, exp_rand):
+            out, score = _attn.keyformer_attention(q, k, v, exp_rand, tau=tau, ref_rounding=True)
+            return out, score.view(q.shape[0], int(model.kv_head_num), k.shape[1])
     else:
         raise NotImplementedError(f"system mi355x has no kernel for case {name!r} "
-                                  "(supported: Attn, Gemma2, H2O, RoCo, SnapKV, Corm)")
+                                  "(supported: Attn, Gemma2, H2O, RoCo, SnapKV, Corm, KeyFormer)")
     return f
 
 

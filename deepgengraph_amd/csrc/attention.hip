@@ -26,6 +26,406 @@ namespace {
 
 using namespace dgg_attn;
 
+// ------------------------------------------------------------------------------------------------
+// Forward kernel.
+// ------------------------------------------------------------------------------------------------
+template <typename T, int D, int BN, bool MASK, bool SOFTCAP, bool REFROUND>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2, 2))) attn_fwd_kernel(AttnParams p) {
+  typedef typename T::scalar S;
+  typedef typename T::vec8 V8;
+  typedef typename T::vec4 V4;
+  constexpr int KP = D + 8;  // padded K row (elements): 16-byte shift per row for the fragment reads
+  constexpr int VP = D + 8;  // padded V row (elements): 16-byte shift per row for the transposing reads
+  constexpr int NKK = D / 16;      // MFMA k-steps over the head dim
+  constexpr int NMB = BN / 32;     // 32-key blocks per tile
+  constexpr int NDB = D / 32;      // 32-wide head-dim blocks of O^T
+  constexpr int NPK = BN / 16;     // MFMA k-steps over keys in P.V
+  constexpr int CHUNKS = BN * D / 8;
+  constexpr int CPT = CHUNKS / kThreads;  // 16-byte chunks per thread per tile (K and V each)
+  static_assert(CHUNKS % kThreads == 0, "tile must split evenly over the workgroup");
+
+  __shared__ __attribute__((aligned(16))) S Ks[2][BN][KP];
+  __shared__ __attribute__((aligned(16))) S Vs[2][BN][VP];
+
+  int qt, bh;
+  map_block(p.n_tiles, p.B * p.Hq, true, qt, bh);
+  const int b = bh / p.Hq, h = bh - b * p.Hq;
+  const int hk = h / p.group;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, r = lane & 31, g = lane >> 5;
+  const int q0 = qt * kBM;
+  const int qi = q0 + 32 * w + r;  // this lane's query row
+  const int tr_krow = (lane & 15) >> 2;                              // key row within a group of 4
+  const int tr_dcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);     // head-dim column within a 32-wide block
+
+  const S* qp = static_cast<const S*>(p.q) + b * p.q_sb + h * p.q_sh;
+  const S* kp = static_cast<const S*>(p.k) + b * p.k_sb + hk * p.k_sh;
+  const S* vp = static_cast<const S*>(p.v) + b * p.v_sb + hk * p.v_sh;
+
+  // Q fragment (B operand of S^T = K.Q^T): lane holds query qi, head-dim elements 16kk + 8g .. +8.
+  V8 qf[NKK];
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk)  // back-to-back loads (rows past the end read the last row, zeroed below)
+    qf[kk] = ld16<V8>(qp + (int64_t)min(qi, p.Sq - 1) * p.q_ss + 16 * kk + 8 * g);
+  // Re-define the Q registers here (after their loads complete) so that the main loop's wait counting does not
+  // treat them as results of outstanding vector-memory loads.
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk) {
+    asm volatile("" : "+v"(qf[kk]));
+    if (qi >= p.Sq) qf[kk] = V8{};
+  }
+
+  // Key range of this query tile.
+  const int q_last = min(q0 + kBM, p.Sq) - 1;
+  int k_begin = 0, k_end = p.Sk;
+  if (p.causal) k_end = min(p.Sk, q_last + p.offset + 1);
+  if (p.window > 0) k_begin = max(0, q0 + p.offset - p.window + 1);
+  const int t_begin = k_begin / BN;
+  const int t_end = k_end > k_begin ? (k_end + BN - 1) / BN : t_begin;
+
+  f32x16 oacc[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i) oacc[i] = f32x16{};
+  float m_run = -INFINITY;  // reference maximum (value units)
+  const float c = score_coeff<SOFTCAP, REFROUND>(p);
+
+  // Global -> register staging of one K/V tile: each thread owns CPT adjacent 16-byte chunks of one key row of
+  // K and of V (coalesced rows; both stay row-major in LDS). Full tiles are addressed through two per-lane
+  // pointers that advance by one tile right before each load (so a pointer register is never rewritten while
+  // loads through it are in flight), the chunk index going into the immediate offset.
+  V8 kreg[CPT], vreg[CPT];
+  constexpr int TPR = (D / 8) / CPT;        // threads per row
+  static_assert(TPR * CPT == D / 8 && kThreads / TPR == BN, "tile mapping");
+  const int k_row0 = tid / TPR, k_c0 = (tid % TPR) * CPT;
+  const int64_t k_step = (int64_t)BN * p.k_ss * (int64_t)sizeof(S), v_step = (int64_t)BN * p.v_ss * (int64_t)sizeof(S);
+  // pointers of tile t_begin - 1 (advanced before use)
+  gptr k_addr = to_gptr(kp + (int64_t)(k_row0 - BN) * p.k_ss + k_c0 * 8) + (int64_t)t_begin * k_step;
+  gptr v_addr = to_gptr(vp + (int64_t)(k_row0 - BN) * p.v_ss + k_c0 * 8) + (int64_t)t_begin * v_step;
+  auto load_full = [&]() {
+    k_addr += k_step;
+    v_addr += v_step;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      kreg[i] = ldg16<V8>(k_addr + 16 * i);
+      vreg[i] = ldg16<V8>(v_addr + 16 * i);
+    }
+  };
+  // Ragged last tile: rows past the end are clamped to the last row (masked, finite: contributes exactly 0).
+  auto load_ragged = [&](int t) {
+    k_addr += k_step;
+    v_addr += v_step;
+    const int kb = t * BN;
+    const int kr = min(k_row0, p.Sk - 1 - kb);  // >= 0 for every loaded tile
+    const S* kt = kp + (int64_t)(kb + kr) * p.k_ss + k_c0 * 8;
+    const S* vt = vp + (int64_t)(kb + kr) * p.v_ss + k_c0 * 8;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      kreg[i] = ld16<V8>(kt + i * 8);
+      vreg[i] = ld16<V8>(vt + i * 8);
+    }
+  };
+  auto tile_full = [&](int t) { return (t + 1) * BN <= p.Sk; };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      *reinterpret_cast<V8*>(&Ks[buf][k_row0][(k_c0 + i) * 8]) = kreg[i];
+      *reinterpret_cast<V8*>(&Vs[buf][k_row0][(k_c0 + i) * 8]) = vreg[i];
+    }
+  };
+
+  if (t_begin < t_end) {
+    if (tile_full(t_begin)) load_full();
+    else load_ragged(t_begin);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  // Visible keys of this lane's query: lo <= key <= hi (bottom-right causal, sliding window, ragged end).
+  int k_hi = p.Sk - 1, k_lo = 0;
+  if (p.causal) k_hi = min(k_hi, qi + p.offset);
+  if (p.window > 0) k_lo = max(k_lo, qi + p.offset - p.window + 1);
+  float l_part[4] = {0.f, 0.f, 0.f, 0.f};  // split row sums (breaks the dependent add chain)
+
+  // One K/V tile: S^T = K.Q^T, scores, online softmax, O^T += V^T.P^T. MASKED tiles compare each key against
+  // the lane's [k_lo, k_hi]; all other tiles run without any mask arithmetic.
+  auto tile = [&](const int t, const int buf, auto masked) {
+    f32x16 sacc[NMB];
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) sacc[mb] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb) {
+        const V8 a = *reinterpret_cast<const V8*>(&Ks[buf][mb * 32 + r][16 * kk + 8 * g]);
+        sacc[mb] = mfma32(a, qf[kk], sacc[mb]);
+      }
+    }
+    // element (mb, j) holds key t*BN + mb*32 + 8*(j/4) + 4g + j%4
+    const int rel_hi = k_hi - (t * BN + 4 * g), rel_lo = k_lo - (t * BN + 4 * g);
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float x = score_value<T, SOFTCAP, REFROUND>(sacc[mb][j], p);
+        if constexpr (decltype(masked)::value) {
+          const int o = mb * 32 + 8 * (j >> 2) + (j & 3);
+          x = (o <= rel_hi && o >= rel_lo) ? x : -INFINITY;
+        }
+        sacc[mb][j] = x;
+        mloc = fmaxf(mloc, x);
+      }
+    }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float m_new = fmaxf(m_run, mloc);
+    const bool need = m_new * c > m_run * c + kRescaleThreshold;
+    if (__any(need)) {
+      const float alpha = need ? fast_exp2((m_run - m_new) * c) : 1.0f;
+      if (need) m_run = m_new;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) l_part[i] *= alpha;
+#pragma unroll
+      for (int i = 0; i < NDB; ++i) oacc[i] *= alpha;
+    }
+    const float mc = m_run == -INFINITY ? 0.f : m_run * c;
+
+    // P = exp2(v*c - m*c), row sums, pack to 16-bit B operands, O^T += V^T . P^T
+#pragma unroll
+    for (int kk = 0; kk < NPK; ++kk) {
+      f32x8 pv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float pe = fast_exp2(fmaf(sacc[kk >> 1][8 * (kk & 1) + e], c, -mc));
+        l_part[e & 3] += pe;
+        pv[e] = pe;
+      }
+      const V8 pb = from_f32x8<V8>(pv);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        // A = V^T rows db*32 + r, keys 16kk + 4g + {0..3} and 16kk + 8 + 4g + {0..3} (the P operand's key order),
+        // gathered from row-major V by the transposing read (lane m of each 16-lane group points at key row
+        // m/4 and head-dim column 4*(m%4) of its 16-column slab).
+        const S* vrow = &Vs[buf][16 * kk + 4 * g + tr_krow][db * 32 + tr_dcol];
+        const V4 lo = tr_read(vrow);
+        const V4 hi = tr_read(vrow + 8 * VP);
+        const V8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        oacc[db] = mfma32(a, pb, oacc[db]);
+      }
+    }
+  };
+
+  // Tiles [t_begin, t_full0) and [t_full1, t_end) straddle the window's lower edge or the causal diagonal (or the
+  // ragged end of K) and evaluate the mask; tiles in between are visible to every row of the workgroup.
+  int t_full0 = t_begin, t_full1 = t_end;
+  if constexpr (MASK) {
+    if (p.window > 0) {  // first tile whose first key is visible to the last row
+      const int lo_last = q_last + p.offset - p.window + 1;
+      t_full0 = lo_last <= 0 ? t_begin : min(t_end, max(t_begin, (lo_last + BN - 1) / BN));
+    }
+    if (p.causal) {  // first tile whose last key is hidden from the first row
+      const int hi_first = q0 + p.offset;  // last key visible to the first row
+      t_full1 = max(t_full0, min(t_end, hi_first < 0 ? t_begin : (hi_first + 1) / BN));
+    }
+  }
+  if (t_full1 > t_full0 && t_full1 * BN > p.Sk) t_full1 = max(t_full0, p.Sk / BN);
+  if (t_full1 < t_full0) t_full1 = t_full0;
+
+  // Full next tiles are prefetched into registers before this tile's compute; the ragged last tile (at most one)
+  // is loaded after it.
+  auto step = [&](const int t, auto masked) {
+    const int buf = (t - t_begin) & 1;
+    const int tn = t + 1;
+    const bool prefetch = tn < t_end && tile_full(tn);
+    if (prefetch) load_full();
+    tile(t, buf, masked);
+    if (tn < t_end) {
+      if (!prefetch) load_ragged(tn);
+      store_tile(buf ^ 1);
+    }
+    __syncthreads();
+  };
+  for (int t = t_begin; t < t_full0; ++t) step(t, std::true_type{});
+  for (int t = t_full0; t < t_full1; ++t) step(t, std::false_type{});
+  for (int t = t_full1; t < t_end; ++t) step(t, std::true_type{});
+  float l_run = (l_part[0] + l_part[1]) + (l_part[2] + l_part[3]);
+
+  // Epilogue: full row sum, normalise, store O (4 consecutive head-dim elements per store) and lse.
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = 1.0f / l_tot;
+  if (qi < p.Sq) {
+    S* op = static_cast<S*>(p.o) + b * p.o_sb + (int64_t)qi * p.o_ss + h * p.o_sh;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        V4 ov;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ov[e] = to_s<S>(oacc[db][4 * jj + e] * inv);
+        *reinterpret_cast<V4*>(op + db * 32 + 8 * jj + 4 * g) = ov;
+      }
+    }
+    if (p.lse != nullptr && g == 0) {
+      const float lse2 = m_run == -INFINITY ? -INFINITY : m_run * c + fast_log2(l_tot);
+      p.lse[(int64_t)bh * p.Sq + qi] = p.lse_base2 ? lse2 : lse2 * kLn2;
+    }
+  }
+}
+
+
+
+// ------------------------------------------------------------------------------------------------
+// KeyFormer pass 1 (kf.py:36-39): the base-2 log-sum-exp of the Gumbel-perturbed scores of each query row,
+//   lse2'[b, h, i] = log2 sum_j exp2(y_ij),  y_ij = (s2_ij - log2 e_ij) / tau,
+// over the keys j the row sees, with s2 the score in the exp2 domain (rounded as the reference rounds when
+// REFROUND) and e the exp_rand input (gumbels = -log(e), kf.py:37). Four waves of 32 rows; S^T = K.Q^T puts one
+// query per lane, so the row reduction stays in the lane (plus one cross-half step). K tiles of 64 keys are staged
+// through double-buffered LDS; exp_rand is read once, as 16-byte loads when VEC (rows 16-byte aligned).
+// ------------------------------------------------------------------------------------------------
+template <typename T, int D, bool MASK, bool REFROUND, bool VEC>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_kf_rowlse_kernel(AttnParams p) {
+  typedef typename T::scalar S;
+  typedef typename T::vec8 V8;
+  constexpr int BN = 64;
+  constexpr int KP = D + 8;       // padded K row: 16-byte shift per row for the fragment reads
+  constexpr int NKK = D / 16;
+  constexpr int NMB = BN / 32;
+  constexpr int CPT = BN * D / 8 / kThreads;  // 16-byte chunks per thread per tile
+  constexpr int TPR = (D / 8) / CPT;          // threads per key row
+  static_assert(CPT * kThreads == BN * D / 8 && kThreads / TPR == BN, "tile mapping");
+  __shared__ __attribute__((aligned(16))) S Ks[2][BN][KP];
+
+  int qt, bh;
+  map_block(p.n_tiles, p.B * p.Hq, true, qt, bh);
+  const int b = bh / p.Hq, h = bh - b * p.Hq;
+  const int hk = h / p.group;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, r = lane & 31, g = lane >> 5;
+  const int q0 = qt * kBM;
+  const int qi = q0 + 32 * w + r;
+  const int qc = min(qi, p.Sq - 1);
+  const S* qp = static_cast<const S*>(p.q) + b * p.q_sb + h * p.q_sh;
+  const S* kp = static_cast<const S*>(p.k) + b * p.k_sb + hk * p.k_sh;
+  const float* erow = p.er + b * p.er_sb + h * p.er_sh + (int64_t)qc * p.er_ss;
+
+  V8 qf[NKK];
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk) qf[kk] = ld16<V8>(qp + (int64_t)qc * p.q_ss + 16 * kk + 8 * g);
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk) {
+    asm volatile("" : "+v"(qf[kk]));
+    if (qi >= p.Sq) qf[kk] = V8{};
+  }
+
+  const int q_last = min(q0 + kBM, p.Sq) - 1;
+  int k_begin = 0, k_end = p.Sk;
+  if (p.causal) k_end = min(p.Sk, q_last + p.offset + 1);
+  if (p.window > 0) k_begin = max(0, q0 + p.offset - p.window + 1);
+  const int t_begin = k_begin / BN;
+  const int t_end = k_end > k_begin ? (k_end + BN - 1) / BN : t_begin;
+  int k_hi = p.Sk - 1, k_lo = 0;
+  if (p.causal) k_hi = min(k_hi, qi + p.offset);
+  if (p.window > 0) k_lo = max(k_lo, qi + p.offset - p.window + 1);
+
+  // K staging: thread tid copies CPT adjacent chunks of key row tid / TPR (rows past the end read the last row).
+  V8 kreg[CPT];
+  const int k_row0 = tid / TPR, k_c0 = (tid % TPR) * CPT;
+  auto load = [&](int t) {
+    const S* src = kp + (int64_t)min(t * BN + k_row0, p.Sk - 1) * p.k_ss + k_c0 * 8;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) kreg[i] = ld16<V8>(src + 8 * i);
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) *reinterpret_cast<V8*>(&Ks[buf][k_row0][(k_c0 + i) * 8]) = kreg[i];
+  };
+
+  const float c = score_coeff<false, REFROUND>(p);
+  float m_run = -INFINITY, l_run = 0.f;
+  // element (mb, j) of the S^T accumulators holds key t*BN + mb*32 + 8*(j/4) + 4g + j%4
+  auto tile = [&](int t, int buf, auto masked) {
+    const int kb = t * BN;
+    f32x4 ev[NMB][4];
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        const int key = kb + mb * 32 + 8 * jq + 4 * g;
+        if (VEC && !decltype(masked)::value) {
+          ev[mb][jq] = *reinterpret_cast<const f32x4*>(erow + key);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ev[mb][jq][e] = erow[min(key + e, p.Sk - 1)];
+        }
+      }
+    f32x16 sacc[NMB];
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) sacc[mb] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk)
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb)
+        sacc[mb] = mfma32(*reinterpret_cast<const V8*>(&Ks[buf][mb * 32 + r][16 * kk + 8 * g]), qf[kk], sacc[mb]);
+    const int rel_hi = k_hi - (kb + 4 * g), rel_lo = k_lo - (kb + 4 * g);
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float x2 = score_value<T, false, REFROUND>(sacc[mb][j], p) * c;
+        float y = (x2 - fast_log2(ev[mb][j >> 2][j & 3])) * p.kf_inv_tau;
+        if constexpr (decltype(masked)::value) {
+          const int o = mb * 32 + 8 * (j >> 2) + (j & 3);
+          y = (o <= rel_hi && o >= rel_lo) ? y : -INFINITY;
+        }
+        sacc[mb][j] = y;
+        mloc = fmaxf(mloc, y);
+      }
+    mloc = half_swap_max(mloc);
+    const float m_new = fmaxf(m_run, mloc);
+    if (m_new > m_run + kRescaleThreshold || (m_run == -INFINITY && m_new > -INFINITY)) {
+      l_run *= fast_exp2(m_run - m_new);  // 0 while m_run is -inf
+      m_run = m_new;
+    }
+    const float mu = m_run == -INFINITY ? 0.f : m_run;
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) l_run += fast_exp2(sacc[mb][j] - mu);
+  };
+
+  // Tiles [t_full0, t_full1) need no mask for any row of the workgroup (as in attn_fwd_kernel).
+  int t_full0 = t_begin, t_full1 = t_end;
+  if constexpr (MASK) {
+    if (p.window > 0) {
+      const int lo_last = q_last + p.offset - p.window + 1;
+      t_full0 = lo_last <= 0 ? t_begin : min(t_end, max(t_begin, (lo_last + BN - 1) / BN));
+    }
+    if (p.causal) {
+      const int hi_first = q0 + p.offset;
+      t_full1 = max(t_full0, min(t_end, hi_first < 0 ? t_begin : (hi_first + 1) / BN));
+    }
+  }
+  if (t_full1 > t_full0 && t_full1 * BN > p.Sk) t_full1 = max(t_full0, p.Sk / BN);
+  if (t_full1 < t_full0) t_full1 = t_full0;
+
+  if (t_begin < t_end) {
+    load(t_begin);
+    store(0);
+  }
+  __syncthreads();
+  auto step = [&](int t, auto masked) {
+    const int buf = (t - t_begin) & 1;
+    const bool more = t + 1 < t_end;
+    if (more) load(t + 1);
+    tile(t, buf, masked);
+    if (more) store(buf ^ 1);
+    __syncthreads();
+  };
+  for (int t = t_begin; t < t_full0; ++t) step(t, std::true_type{});
+  for (int t = t_full0; t < t_full1; ++t) step(t, std::false_type{});
+  for (int t = t_full1; t < t_end; ++t) step(t, std::true_type{});
+
+  const float l_tot = half_swap_sum(l_run);
+  if (qi < p.Sq && g == 0) p.lse[(int64_t)bh * p.Sq + qi] = m_run == -INFINITY ? -INFINITY : m_run + fast_log2(l_tot);
+}
 
 // NQB: 32-row query blocks per wave (each K / V fragment feeds NQB MFMAs); NW: waves per workgroup; BN: keys
 // per tile; NSTAGE: tiles in the LDS ring; OCC: waves per SIMD the register budget is sized for. FASTSUM: the row
@@ -512,6 +912,7 @@ __global__ void __launch_bounds__(kThreads) attn_colsum_kernel(AttnParams p) {
 
   ColAcc<EPI> acc;
   const int kjc = min(kj, p.Sk - 1);
+  const float* erp = EPI == kColKF ? p.er + b * p.er_sb + h * p.er_sh : nullptr;  // KeyFormer exp_rand of (b, h)
   for (int t = t_begin; t < t_end; ++t) {
     const int buf = (t - t_begin) & 1;
     const bool has_next = t + 1 < t_end;
@@ -541,8 +942,12 @@ __global__ void __launch_bounds__(kThreads) attn_colsum_kernel(AttnParams p) {
       for (int j = 0; j < 16; ++j) {
         const int row = mb * 32 + 8 * (j >> 2) + 4 * g + (j & 3);
         const float x = score_value<T, SOFTCAP, REFROUND>(sacc[mb][j], p);
-        float pe = fast_exp2(fmaf(x, c, -Ls[buf][row]));
         const int qg = qb + row;
+        float pe;
+        if constexpr (EPI == kColKF)
+          pe = kf_prob(x * c, erp[(int64_t)min(qg, p.Sq - 1) * p.er_ss + kjc], Ls[buf][row], p);
+        else
+          pe = fast_exp2(fmaf(x, c, -Ls[buf][row]));
         if (need_mask) {
           bool ok = qg < p.Sq && kj < p.Sk;
           if constexpr (MASK) {
@@ -691,6 +1096,7 @@ attn_colsum_d128_kernel(AttnParams p) {
   const float c = PK ? kLog2e : score_coeff<SOFTCAP, REFROUND>(p);
   ColAcc<EPI> acc;
   const int kjc = min(kj, p.Sk - 1);
+  const float* erp = EPI == kColKF ? p.er + b * p.er_sb + h * p.er_sh : nullptr;  // KeyFormer exp_rand of (b, h)
 
   auto tile = [&](const int t, auto masked) {
     const uint32_t st = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B);
@@ -724,8 +1130,12 @@ attn_colsum_d128_kernel(AttnParams p) {
         if constexpr (PK) x = (float)hs[j >> 1][j & 1];
         else x = score_value<T, SOFTCAP, REFROUND>(sacc[mb][j], p);
         const float l2 = LSE2 ? lv[j >> 2][j & 3] : lv[j >> 2][j & 3] * kLog2e;
-        float pe = fast_exp2(fmaf(x, c, -l2));
         const int o = 32 * mb + 8 * (j >> 2) + (j & 3);
+        float pe;
+        if constexpr (EPI == kColKF)
+          pe = kf_prob(x * c, erp[(int64_t)min(t * BQ + 4 * g + o, p.Sq - 1) * p.er_ss + kjc], l2, p);
+        else
+          pe = fast_exp2(fmaf(x, c, -l2));
         bool valid = true;
         if constexpr (decltype(masked)::value) {
           valid = o < rows_left;
@@ -876,6 +1286,7 @@ template <typename T, int D>
 void pick_col(const AttnParams& p, bool ref, int epi, hipStream_t st) {
   if (epi == kColSumSq) return pick_col_epi<T, D, kColSumSq>(p, ref, st);
   if (epi == kColAnyGe) return pick_col_epi<T, D, kColAnyGe>(p, ref, st);
+  if (epi == kColKF) return pick_col_epi<T, D, kColKF>(p, ref, st);
   const bool mask = p.causal || p.window > 0;
   const bool sc = p.softcap > 0.f;
   if (mask) {
@@ -884,6 +1295,24 @@ void pick_col(const AttnParams& p, bool ref, int epi, hipStream_t st) {
   } else {
     if (sc) pick_col_ref<T, D, false, true>(p, ref, st);
     else pick_col_ref<T, D, false, false>(p, ref, st);
+  }
+}
+
+template <typename T, int D, bool MASK, bool REFROUND>
+void launch_kf_rowlse(const AttnParams& p, bool vec, hipStream_t st) {
+  const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
+  if (vec) hipLaunchKernelGGL((attn_kf_rowlse_kernel<T, D, MASK, REFROUND, true>), dim3(grid), dim3(kThreads), 0, st, p);
+  else hipLaunchKernelGGL((attn_kf_rowlse_kernel<T, D, MASK, REFROUND, false>), dim3(grid), dim3(kThreads), 0, st, p);
+}
+template <typename T, int D>
+void pick_kf_rowlse(const AttnParams& p, bool ref, bool vec, hipStream_t st) {
+  const bool mask = p.causal || p.window > 0;
+  if (mask) {
+    if (ref) launch_kf_rowlse<T, D, true, true>(p, vec, st);
+    else launch_kf_rowlse<T, D, true, false>(p, vec, st);
+  } else {
+    if (ref) launch_kf_rowlse<T, D, false, true>(p, vec, st);
+    else launch_kf_rowlse<T, D, false, false>(p, vec, st);
   }
 }
 
@@ -1026,6 +1455,93 @@ int colscore(const char* op, const void* q, const void* k, const float* lse, int
   return dgg::check_launch(op);
 }
 }  // namespace
+
+namespace {
+// exp_rand [B, Hq, Sq, Sk] fp32 with element strides er_strides = {batch, head, row} and unit key stride.
+int validate_exp_rand(const char* op, const float* er, const int64_t* er_strides, int64_t Sq, float tau) {
+  DGG_REQUIRE(er != nullptr && er_strides != nullptr, DGG_ERR_NULL, "%s: null exp_rand / strides", op);
+  DGG_REQUIRE(((uintptr_t)er & 3u) == 0, DGG_ERR_ALIGN, "%s: exp_rand must be 4-byte aligned", op);
+  for (int i = 0; i < 3; ++i)
+    DGG_REQUIRE(er_strides[i] >= 0 && er_strides[i] < (1ll << 40), DGG_ERR_STRIDE, "%s: exp_rand stride[%d] invalid", op,
+                i);
+  DGG_REQUIRE(Sq <= 1 || er_strides[2] > 0, DGG_ERR_STRIDE, "%s: exp_rand row stride must be > 0", op);
+  DGG_REQUIRE(std::isfinite(tau) && tau > 0.f, DGG_ERR_SHAPE, "%s: tau must be finite and > 0", op);
+  return DGG_OK;
+}
+void set_exp_rand(AttnParams& p, const float* er, const int64_t* er_strides, float tau) {
+  p.er = er;
+  p.er_sb = er_strides[0];
+  p.er_sh = er_strides[1];
+  p.er_ss = er_strides[2];
+  p.kf_inv_tau = 1.0f / tau;
+}
+}  // namespace
+
+extern "C" int dgg_attn_kf_rowlse(const void* q, const void* k, const float* exp_rand, const int64_t* er_strides,
+                                  float* lse2, int64_t B, int64_t Sq, int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D,
+                                  const int64_t* strides, float scale, float tau, int64_t window, uint32_t flags,
+                                  int dtype, void* stream) {
+  const char* op = "attn_kf_rowlse";
+  if (int rc = validate_attn(op, q, k, B, Sq, Sk, Hq, Hkv, D, strides, 6, scale, 0.f, window, dtype)) return rc;
+  if (B == 0 || Sq == 0) return DGG_OK;
+  DGG_REQUIRE(lse2 != nullptr, DGG_ERR_NULL, "%s: null lse output", op);
+  DGG_REQUIRE(Sk > 0, DGG_ERR_SHAPE, "%s: Sk must be > 0", op);
+  if (int rc = validate_exp_rand(op, exp_rand, er_strides, Sq, tau)) return rc;
+  AttnParams p = make_params(q, k, nullptr, nullptr, B, Sq, Sk, Hq, Hkv, scale, 0.f, window, flags);
+  p.lse = lse2;
+  p.q_sb = strides[0]; p.q_ss = strides[1]; p.q_sh = strides[2];
+  p.k_sb = strides[3]; p.k_ss = strides[4]; p.k_sh = strides[5];
+  set_exp_rand(p, exp_rand, er_strides, tau);
+  p.n_tiles = (int)((Sq + kBM - 1) / kBM);
+  const bool vec = dgg::aligned16(exp_rand) && er_strides[0] % 4 == 0 && er_strides[1] % 4 == 0 && er_strides[2] % 4 == 0;
+  const bool ref = (flags & DGG_ATTN_REF_ROUNDING) != 0;
+  hipStream_t st = dgg::as_stream(stream);
+  if (dtype == DGG_BF16) {
+    if (D == 64) pick_kf_rowlse<BF16, 64>(p, ref, vec, st);
+    else if (D == 128) pick_kf_rowlse<BF16, 128>(p, ref, vec, st);
+    else pick_kf_rowlse<BF16, 256>(p, ref, vec, st);
+  } else {
+    if (D == 64) pick_kf_rowlse<F16, 64>(p, ref, vec, st);
+    else if (D == 128) pick_kf_rowlse<F16, 128>(p, ref, vec, st);
+    else pick_kf_rowlse<F16, 256>(p, ref, vec, st);
+  }
+  return dgg::check_launch(op);
+}
+
+extern "C" int dgg_attn_kf_colsum(const void* q, const void* k, const float* exp_rand, const int64_t* er_strides,
+                                  const float* lse2, float* kf_score, int64_t B, int64_t Sq, int64_t Sk, int64_t Hq,
+                                  int64_t Hkv, int64_t D, const int64_t* strides, float scale, float tau,
+                                  int64_t window, uint32_t flags, int dtype, void* stream) {
+  const char* op = "attn_kf_colsum";
+  if (int rc = validate_attn(op, q, k, B, Sq, Sk, Hq, Hkv, D, strides, 6, scale, 0.f, window, dtype)) return rc;
+  if (B == 0 || Sk == 0) return DGG_OK;
+  DGG_REQUIRE(kf_score != nullptr, DGG_ERR_NULL, "%s: null output", op);
+  DGG_REQUIRE(Sq == 0 || lse2 != nullptr, DGG_ERR_NULL, "%s: null lse pointer", op);
+  if (Sq > 0)
+    if (int rc = validate_exp_rand(op, exp_rand, er_strides, Sq, tau)) return rc;
+  // The row lse of the perturbed scores is base 2 (as dgg_attn_kf_rowlse writes it).
+  AttnParams p = make_params(q, k, nullptr, nullptr, B, Sq, Sk, Hq, Hkv, scale, 0.f, window,
+                             flags | DGG_ATTN_LSE_BASE2);
+  p.lse = const_cast<float*>(lse2);
+  p.colsum = kf_score;
+  p.q_sb = strides[0]; p.q_ss = strides[1]; p.q_sh = strides[2];
+  p.k_sb = strides[3]; p.k_ss = strides[4]; p.k_sh = strides[5];
+  if (Sq > 0) set_exp_rand(p, exp_rand, er_strides, tau);
+  const int64_t bk = D == 128 ? kC128BK : kCBK;
+  p.n_tiles = (int)((Sk + bk - 1) / bk);
+  const bool ref = (flags & DGG_ATTN_REF_ROUNDING) != 0;
+  hipStream_t st = dgg::as_stream(stream);
+  if (dtype == DGG_BF16) {
+    if (D == 64) pick_col<BF16, 64>(p, ref, kColKF, st);
+    else if (D == 128) pick_col<BF16, 128>(p, ref, kColKF, st);
+    else pick_col<BF16, 256>(p, ref, kColKF, st);
+  } else {
+    if (D == 64) pick_col<F16, 64>(p, ref, kColKF, st);
+    else if (D == 128) pick_col<F16, 128>(p, ref, kColKF, st);
+    else pick_col<F16, 256>(p, ref, kColKF, st);
+  }
+  return dgg::check_launch(op);
+}
 
 extern "C" int dgg_attn_colsum(const void* q, const void* k, const float* lse, float* colsum, int64_t B, int64_t Sq,
                                int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides, float scale,

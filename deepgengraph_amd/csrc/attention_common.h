@@ -27,6 +27,9 @@ struct AttnParams {
   const float* thr;      // [Sq, Sk] thresholds, row stride thr_rs (kColAnyGe)
   int64_t thr_rs;
   uint8_t* any_out;      // [B, Hq, Sk] (kColAnyGe)
+  const float* er;       // KeyFormer exp_rand [B, Hq, Sq, Sk], element strides er_sb, er_sh, er_ss (unit key stride)
+  int64_t er_sb, er_sh, er_ss;
+  float kf_inv_tau;      // 1 / tau of the perturbed softmax
   int64_t q_sb, q_ss, q_sh;
   int64_t k_sb, k_ss, k_sh;
   int64_t v_sb, v_ss, v_sh;
@@ -47,6 +50,13 @@ struct AttnParams {
   float sc_a;    // 2 * scale / softcap * log2(e)
   float sc_b;    // softcap * log2(e)
 };
+
+// Probability of the perturbed score for KeyFormer: x2 = the score in the exp2 domain, e = exp_rand, l2 = the
+// perturbed row lse in base 2: exp2((x2 - log2 e) / tau - l2) (kf.py:37-39: gumbels = -log(e),
+// softmax((scores + gumbels) / tau)).
+__device__ __forceinline__ float kf_prob(float x2, float e, float l2, const AttnParams& p) {
+  return __builtin_amdgcn_exp2f(fmaf(x2 - __builtin_amdgcn_logf(e), p.kf_inv_tau, -l2));
+}
 
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -119,7 +129,9 @@ __device__ __forceinline__ float score_coeff(const AttnParams& p) {
 
 // Column epilogues of the column-sum kernels: H2O / SnapKV sum p (h2o.py:35-36, snapkv.py:36-37), RoCo also sums
 // p^2 (roco.py:43-47), Corm ORs p >= threshold[i][j] over the queries (corm.py:35-37).
-enum ColEpi { kColSum = 0, kColSumSq = 1, kColAnyGe = 2 };
+// KeyFormer (kf.py:36-40) sums the probabilities of the Gumbel-perturbed scores (s - ln e) / tau instead
+// (kColKF: the column kernels then read the perturbed row lse and the exp_rand input e).
+enum ColEpi { kColSum = 0, kColSumSq = 1, kColAnyGe = 2, kColKF = 3 };
 template <int EPI>
 struct ColAcc {
   float s = 0.f, s2 = 0.f;
@@ -175,250 +187,6 @@ __device__ __forceinline__ void map_block(int n_tiles, int bh_count, bool revers
   }
   tile = reverse ? n_tiles - 1 - t_major : t_major;
   bh = bh_minor;
-}
-
-// ------------------------------------------------------------------------------------------------
-// Forward kernel.
-// ------------------------------------------------------------------------------------------------
-template <typename T, int D, int BN, bool MASK, bool SOFTCAP, bool REFROUND>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2, 2))) attn_fwd_kernel(AttnParams p) {
-  typedef typename T::scalar S;
-  typedef typename T::vec8 V8;
-  typedef typename T::vec4 V4;
-  constexpr int KP = D + 8;  // padded K row (elements): 16-byte shift per row for the fragment reads
-  constexpr int VP = D + 8;  // padded V row (elements): 16-byte shift per row for the transposing reads
-  constexpr int NKK = D / 16;      // MFMA k-steps over the head dim
-  constexpr int NMB = BN / 32;     // 32-key blocks per tile
-  constexpr int NDB = D / 32;      // 32-wide head-dim blocks of O^T
-  constexpr int NPK = BN / 16;     // MFMA k-steps over keys in P.V
-  constexpr int CHUNKS = BN * D / 8;
-  constexpr int CPT = CHUNKS / kThreads;  // 16-byte chunks per thread per tile (K and V each)
-  static_assert(CHUNKS % kThreads == 0, "tile must split evenly over the workgroup");
-
-  __shared__ __attribute__((aligned(16))) S Ks[2][BN][KP];
-  __shared__ __attribute__((aligned(16))) S Vs[2][BN][VP];
-
-  int qt, bh;
-  map_block(p.n_tiles, p.B * p.Hq, true, qt, bh);
-  const int b = bh / p.Hq, h = bh - b * p.Hq;
-  const int hk = h / p.group;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, r = lane & 31, g = lane >> 5;
-  const int q0 = qt * kBM;
-  const int qi = q0 + 32 * w + r;  // this lane's query row
-  const int tr_krow = (lane & 15) >> 2;                              // key row within a group of 4
-  const int tr_dcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);     // head-dim column within a 32-wide block
-
-  const S* qp = static_cast<const S*>(p.q) + b * p.q_sb + h * p.q_sh;
-  const S* kp = static_cast<const S*>(p.k) + b * p.k_sb + hk * p.k_sh;
-  const S* vp = static_cast<const S*>(p.v) + b * p.v_sb + hk * p.v_sh;
-
-  // Q fragment (B operand of S^T = K.Q^T): lane holds query qi, head-dim elements 16kk + 8g .. +8.
-  V8 qf[NKK];
-#pragma unroll
-  for (int kk = 0; kk < NKK; ++kk)  // back-to-back loads (rows past the end read the last row, zeroed below)
-    qf[kk] = ld16<V8>(qp + (int64_t)min(qi, p.Sq - 1) * p.q_ss + 16 * kk + 8 * g);
-  // Re-define the Q registers here (after their loads complete) so that the main loop's wait counting does not
-  // treat them as results of outstanding vector-memory loads.
-#pragma unroll
-  for (int kk = 0; kk < NKK; ++kk) {
-    asm volatile("" : "+v"(qf[kk]));
-    if (qi >= p.Sq) qf[kk] = V8{};
-  }
-
-  // Key range of this query tile.
-  const int q_last = min(q0 + kBM, p.Sq) - 1;
-  int k_begin = 0, k_end = p.Sk;
-  if (p.causal) k_end = min(p.Sk, q_last + p.offset + 1);
-  if (p.window > 0) k_begin = max(0, q0 + p.offset - p.window + 1);
-  const int t_begin = k_begin / BN;
-  const int t_end = k_end > k_begin ? (k_end + BN - 1) / BN : t_begin;
-
-  f32x16 oacc[NDB];
-#pragma unroll
-  for (int i = 0; i < NDB; ++i) oacc[i] = f32x16{};
-  float m_run = -INFINITY;  // reference maximum (value units)
-  const float c = score_coeff<SOFTCAP, REFROUND>(p);
-
-  // Global -> register staging of one K/V tile: each thread owns CPT adjacent 16-byte chunks of one key row of
-  // K and of V (coalesced rows; both stay row-major in LDS). Full tiles are addressed through two per-lane
-  // pointers that advance by one tile right before each load (so a pointer register is never rewritten while
-  // loads through it are in flight), the chunk index going into the immediate offset.
-  V8 kreg[CPT], vreg[CPT];
-  constexpr int TPR = (D / 8) / CPT;        // threads per row
-  static_assert(TPR * CPT == D / 8 && kThreads / TPR == BN, "tile mapping");
-  const int k_row0 = tid / TPR, k_c0 = (tid % TPR) * CPT;
-  const int64_t k_step = (int64_t)BN * p.k_ss * (int64_t)sizeof(S), v_step = (int64_t)BN * p.v_ss * (int64_t)sizeof(S);
-  // pointers of tile t_begin - 1 (advanced before use)
-  gptr k_addr = to_gptr(kp + (int64_t)(k_row0 - BN) * p.k_ss + k_c0 * 8) + (int64_t)t_begin * k_step;
-  gptr v_addr = to_gptr(vp + (int64_t)(k_row0 - BN) * p.v_ss + k_c0 * 8) + (int64_t)t_begin * v_step;
-  auto load_full = [&]() {
-    k_addr += k_step;
-    v_addr += v_step;
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      kreg[i] = ldg16<V8>(k_addr + 16 * i);
-      vreg[i] = ldg16<V8>(v_addr + 16 * i);
-    }
-  };
-  // Ragged last tile: rows past the end are clamped to the last row (masked, finite: contributes exactly 0).
-  auto load_ragged = [&](int t) {
-    k_addr += k_step;
-    v_addr += v_step;
-    const int kb = t * BN;
-    const int kr = min(k_row0, p.Sk - 1 - kb);  // >= 0 for every loaded tile
-    const S* kt = kp + (int64_t)(kb + kr) * p.k_ss + k_c0 * 8;
-    const S* vt = vp + (int64_t)(kb + kr) * p.v_ss + k_c0 * 8;
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      kreg[i] = ld16<V8>(kt + i * 8);
-      vreg[i] = ld16<V8>(vt + i * 8);
-    }
-  };
-  auto tile_full = [&](int t) { return (t + 1) * BN <= p.Sk; };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      *reinterpret_cast<V8*>(&Ks[buf][k_row0][(k_c0 + i) * 8]) = kreg[i];
-      *reinterpret_cast<V8*>(&Vs[buf][k_row0][(k_c0 + i) * 8]) = vreg[i];
-    }
-  };
-
-  if (t_begin < t_end) {
-    if (tile_full(t_begin)) load_full();
-    else load_ragged(t_begin);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  // Visible keys of this lane's query: lo <= key <= hi (bottom-right causal, sliding window, ragged end).
-  int k_hi = p.Sk - 1, k_lo = 0;
-  if (p.causal) k_hi = min(k_hi, qi + p.offset);
-  if (p.window > 0) k_lo = max(k_lo, qi + p.offset - p.window + 1);
-  float l_part[4] = {0.f, 0.f, 0.f, 0.f};  // split row sums (breaks the dependent add chain)
-
-  // One K/V tile: S^T = K.Q^T, scores, online softmax, O^T += V^T.P^T. MASKED tiles compare each key against
-  // the lane's [k_lo, k_hi]; all other tiles run without any mask arithmetic.
-  auto tile = [&](const int t, const int buf, auto masked) {
-    f32x16 sacc[NMB];
-#pragma unroll
-    for (int mb = 0; mb < NMB; ++mb) sacc[mb] = f32x16{};
-#pragma unroll
-    for (int kk = 0; kk < NKK; ++kk) {
-#pragma unroll
-      for (int mb = 0; mb < NMB; ++mb) {
-        const V8 a = *reinterpret_cast<const V8*>(&Ks[buf][mb * 32 + r][16 * kk + 8 * g]);
-        sacc[mb] = mfma32(a, qf[kk], sacc[mb]);
-      }
-    }
-    // element (mb, j) holds key t*BN + mb*32 + 8*(j/4) + 4g + j%4
-    const int rel_hi = k_hi - (t * BN + 4 * g), rel_lo = k_lo - (t * BN + 4 * g);
-    float mloc = -INFINITY;
-#pragma unroll
-    for (int mb = 0; mb < NMB; ++mb) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        float x = score_value<T, SOFTCAP, REFROUND>(sacc[mb][j], p);
-        if constexpr (decltype(masked)::value) {
-          const int o = mb * 32 + 8 * (j >> 2) + (j & 3);
-          x = (o <= rel_hi && o >= rel_lo) ? x : -INFINITY;
-        }
-        sacc[mb][j] = x;
-        mloc = fmaxf(mloc, x);
-      }
-    }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float m_new = fmaxf(m_run, mloc);
-    const bool need = m_new * c > m_run * c + kRescaleThreshold;
-    if (__any(need)) {
-      const float alpha = need ? fast_exp2((m_run - m_new) * c) : 1.0f;
-      if (need) m_run = m_new;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) l_part[i] *= alpha;
-#pragma unroll
-      for (int i = 0; i < NDB; ++i) oacc[i] *= alpha;
-    }
-    const float mc = m_run == -INFINITY ? 0.f : m_run * c;
-
-    // P = exp2(v*c - m*c), row sums, pack to 16-bit B operands, O^T += V^T . P^T
-#pragma unroll
-    for (int kk = 0; kk < NPK; ++kk) {
-      f32x8 pv;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float pe = fast_exp2(fmaf(sacc[kk >> 1][8 * (kk & 1) + e], c, -mc));
-        l_part[e & 3] += pe;
-        pv[e] = pe;
-      }
-      const V8 pb = from_f32x8<V8>(pv);
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        // A = V^T rows db*32 + r, keys 16kk + 4g + {0..3} and 16kk + 8 + 4g + {0..3} (the P operand's key order),
-        // gathered from row-major V by the transposing read (lane m of each 16-lane group points at key row
-        // m/4 and head-dim column 4*(m%4) of its 16-column slab).
-        const S* vrow = &Vs[buf][16 * kk + 4 * g + tr_krow][db * 32 + tr_dcol];
-        const V4 lo = tr_read(vrow);
-        const V4 hi = tr_read(vrow + 8 * VP);
-        const V8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        oacc[db] = mfma32(a, pb, oacc[db]);
-      }
-    }
-  };
-
-  // Tiles [t_begin, t_full0) and [t_full1, t_end) straddle the window's lower edge or the causal diagonal (or the
-  // ragged end of K) and evaluate the mask; tiles in between are visible to every row of the workgroup.
-  int t_full0 = t_begin, t_full1 = t_end;
-  if constexpr (MASK) {
-    if (p.window > 0) {  // first tile whose first key is visible to the last row
-      const int lo_last = q_last + p.offset - p.window + 1;
-      t_full0 = lo_last <= 0 ? t_begin : min(t_end, max(t_begin, (lo_last + BN - 1) / BN));
-    }
-    if (p.causal) {  // first tile whose last key is hidden from the first row
-      const int hi_first = q0 + p.offset;  // last key visible to the first row
-      t_full1 = max(t_full0, min(t_end, hi_first < 0 ? t_begin : (hi_first + 1) / BN));
-    }
-  }
-  if (t_full1 > t_full0 && t_full1 * BN > p.Sk) t_full1 = max(t_full0, p.Sk / BN);
-  if (t_full1 < t_full0) t_full1 = t_full0;
-
-  // Full next tiles are prefetched into registers before this tile's compute; the ragged last tile (at most one)
-  // is loaded after it.
-  auto step = [&](const int t, auto masked) {
-    const int buf = (t - t_begin) & 1;
-    const int tn = t + 1;
-    const bool prefetch = tn < t_end && tile_full(tn);
-    if (prefetch) load_full();
-    tile(t, buf, masked);
-    if (tn < t_end) {
-      if (!prefetch) load_ragged(tn);
-      store_tile(buf ^ 1);
-    }
-    __syncthreads();
-  };
-  for (int t = t_begin; t < t_full0; ++t) step(t, std::true_type{});
-  for (int t = t_full0; t < t_full1; ++t) step(t, std::false_type{});
-  for (int t = t_full1; t < t_end; ++t) step(t, std::true_type{});
-  float l_run = (l_part[0] + l_part[1]) + (l_part[2] + l_part[3]);
-
-  // Epilogue: full row sum, normalise, store O (4 consecutive head-dim elements per store) and lse.
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  const float inv = 1.0f / l_tot;
-  if (qi < p.Sq) {
-    S* op = static_cast<S*>(p.o) + b * p.o_sb + (int64_t)qi * p.o_ss + h * p.o_sh;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        V4 ov;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ov[e] = to_s<S>(oacc[db][4 * jj + e] * inv);
-        *reinterpret_cast<V4*>(op + db * 32 + 8 * jj + 4 * g) = ov;
-      }
-    }
-    if (p.lse != nullptr && g == 0) {
-      const float lse2 = m_run == -INFINITY ? -INFINITY : m_run * c + fast_log2(l_tot);
-      p.lse[(int64_t)bh * p.Sq + qi] = p.lse_base2 ? lse2 : lse2 * kLn2;
-    }
-  }
 }
 
 // ------------------------------------------------------------------------------------------------

@@ -128,6 +128,26 @@ int dgg_attn_colscore(const void* q, const void* k, const float* lse, int epilog
                       int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides, float scale, float softcap,
                       int64_t window, uint32_t flags, int dtype, void* stream);
 
+/* KeyFormer (deepgengraph_exp/cases/kernels/kf.py:18-40), which sums over the queries the softmax of the
+ * Gumbel-perturbed scores kf = softmax((scores + gumbels) / tau) with gumbels = -log(exp_rand) (kf.py:36-40):
+ * two passes after the plain forward (dgg_attn_prefill gives the case's `out`).
+ *   dgg_attn_kf_rowlse: lse2[b,h,i] = log2 sum_j exp((s[b,h,i,j] - ln exp_rand[b,h,i,j]) / tau) over the keys
+ *     row i sees (-inf for a row that sees none); fp32 [B, Hq, Sq] contiguous, base 2.
+ *   dgg_attn_kf_colsum: kf_score[b,h,j] = sum_i exp((s - ln exp_rand) / tau - lse2 ln 2), fp32 [B, Hq, Sk]
+ *     contiguous, from the lse2 of the first pass.
+ * s = q.k^T * scale as dgg_attn_prefill's scores (DGG_ATTN_REF_ROUNDING rounds them as the reference does,
+ * kf.py:34), causal / window as there; no soft-cap. exp_rand: fp32 [B, Hq, Sq, Sk] with element strides
+ * er_strides = {batch, head, row} and unit key stride, 4-byte aligned (16-byte aligned rows read faster);
+ * values > 0. tau > 0. Sk >= 1. Other arguments as dgg_attn_colsum. The reference function replaced here is
+ * the eager KeyFormer.forward; its compile()-produced callable is what deepgengraph_amd.compile returns. */
+int dgg_attn_kf_rowlse(const void* q, const void* k, const float* exp_rand, const int64_t* er_strides, float* lse2,
+                       int64_t B, int64_t Sq, int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides,
+                       float scale, float tau, int64_t window, uint32_t flags, int dtype, void* stream);
+int dgg_attn_kf_colsum(const void* q, const void* k, const float* exp_rand, const int64_t* er_strides,
+                       const float* lse2, float* kf_score, int64_t B, int64_t Sq, int64_t Sk, int64_t Hq, int64_t Hkv,
+                       int64_t D, const int64_t* strides, float scale, float tau, int64_t window, uint32_t flags,
+                       int dtype, void* stream);
+
 /* SnapKV pooling of the column sums (snapkv.py:38: F.avg_pool1d(kernel_size, padding = kernel_size // 2,
  * stride 1, count_include_pad)): out[r][j] = sum_{|t| <= kernel_size/2} in[r][j+t] / kernel_size with zeros
  * outside [0, n). in / out fp32 [rows, n] contiguous, not aliased; kernel_size odd. */

@@ -172,6 +172,38 @@ def corm(q, k, v, corm_mask, *, q_chunk=256):
     return out.transpose(1, 2).contiguous(), hit, lse
 
 
+def keyformer(q, k, v, exp_rand, *, tau=1.5, q_chunk=256):
+    """KeyFormer.forward (deepgengraph_exp/cases/kernels/kf.py:18-40): causal attention plus
+    kf_score[b, h, j] = sum_i softmax_j((scores + gumbels) / tau)[i, j] with gumbels = -log(exp_rand) (kf.py:36-40),
+    where `scores` are the dtype-rounded, masked scores (kf.py:29-30) taken to fp32; exp_rand fp32 [B, H, Sq, Sk].
+    Returns (out, kf_score, lse2p) with lse2p the base-2 log-sum-exp of the perturbed rows [B, H, Sq]."""
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    assert k.shape[2] == H, "KeyFormer is multi-head attention (kf.py:16)"
+    dt = q.dtype
+    qt, kt, vt = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    kT = kt.transpose(-2, -1)
+    out = torch.empty(B, H, Sq, D, dtype=dt)
+    score = torch.zeros(B, H, Sk, dtype=torch.float32)
+    lse2p = torch.empty(B, H, Sq, dtype=torch.float32)
+    for i0 in range(0, Sq, q_chunk):
+        n = min(q_chunk, Sq - i0)
+        scores = torch.matmul(qt[:, :, i0:i0 + n], kT) / math.sqrt(D)  # kf.py:29
+        scores = scores.masked_fill(_mask(i0, n, Sq, Sk, True, None), float("-inf"))  # kf.py:30
+        probs = torch.softmax(scores.float(), dim=-1)  # kf.py:31
+        out[:, :, i0:i0 + n] = torch.matmul(probs.to(dt), vt)  # kf.py:32
+        gumbels = -exp_rand[:, :, i0:i0 + n].log()  # kf.py:36-37
+        pert = (scores.float() + gumbels) / tau  # kf.py:38
+        score += torch.softmax(pert, dim=-1).sum(dim=2)  # kf.py:39-40
+        lse2p[:, :, i0:i0 + n] = torch.logsumexp(pert, dim=-1) / math.log(2.0)
+    return out.transpose(1, 2).contiguous(), score, lse2p
+
+
+def exp_rand(B: int, H: int, Sq: int, Sk: int, generator: torch.Generator | None = None) -> torch.Tensor:
+    """KeyFormer.prepare's exp_rand (kf.py:48): 1 + |N(0, 1)|, fp32 [B, H, Sq, Sk]."""
+    return 1 + torch.randn(B, H, Sq, Sk, generator=generator, dtype=torch.float32).abs()
+
+
 def corm_mask(q_len: int, kv_len: int) -> torch.Tensor:
     """Corm.prepare's threshold (corm.py:47-49): row i of ones divided by i + 1, fp32 [q_len, kv_len]."""
     m = torch.ones(q_len, kv_len, dtype=torch.float32)

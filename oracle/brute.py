@@ -96,6 +96,32 @@ def colscores(q, k, *, thr=None):
     return s1, s2, hit
 
 
+def keyformer_colsum(q, k, exp_rand, *, tau):
+    """KeyFormer column sums in float64 loops: sum_i softmax_j((s_ij - ln e_ij) / tau) over the causal keys
+    (kf.py:36-40), with s_ij = q_i . k_j / sqrt(D) unrounded."""
+    B, Sq, H, D = len(q), len(q[0]), len(q[0][0]), len(q[0][0][0])
+    Sk = len(k[0])
+    scale = 1.0 / math.sqrt(D)
+    off = Sk - Sq
+    cs = [[[0.0] * Sk for _ in range(H)] for _ in range(B)]
+    for b in range(B):
+        for h in range(H):
+            for i in range(Sq):
+                ys = {}
+                for j in range(Sk):
+                    if j > i + off:
+                        continue
+                    s = sum(float(q[b][i][h][d]) * float(k[b][j][h][d]) for d in range(D)) * scale
+                    ys[j] = (s - math.log(float(exp_rand[b][h][i][j]))) / tau
+                if not ys:
+                    continue
+                m = max(ys.values())
+                den = sum(math.exp(y - m) for y in ys.values())
+                for j, y in ys.items():
+                    cs[b][h][j] += math.exp(y - m) / den
+    return cs
+
+
 def avg_pool(row, ks):
     """Mean over the window [j - ks//2, j + ks//2] of a list, zeros outside, divided by ks."""
     n, h = len(row), ks // 2

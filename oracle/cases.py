@@ -1,7 +1,7 @@
 """The reference's attention case modules restated on the CPU oracle — TEST INFRASTRUCTURE ONLY.
 
 Same class names, constructor arguments and attributes as deepgengraph_exp/cases/kernels/{attn,gemma2,h2o,roco,
-snapkv,corm}.py,
+snapkv,corm,kf}.py,
 so that tests can hand them to deepgengraph_amd.compile.compile() exactly as run_kernel.py:44-78 does. forward()
 evaluates the oracle (oracle/attention.py) on CPU copies of the inputs and returns CPU tensors.
 """
@@ -97,3 +97,22 @@ class Corm(_Case):
     def forward(self, q, k, v, corm_mask):
         out, hit, _ = _oa.corm(q.cpu(), k.cpu(), v.cpu(), corm_mask.cpu())
         return out, hit
+
+
+class KeyFormer(_Case):
+    """deepgengraph_exp/cases/kernels/kf.py:7-60 (prepare adds exp_rand = 1 + |N(0, 1)|, kf.py:48)."""
+    OUTPUTS = ("out", "kf_score")
+
+    def __init__(self, tau=1.5, kv_head_num=32, head_num=32, head_dim=128):
+        super().__init__(kv_head_num, head_num, head_dim)
+        self.tau = tau
+
+    def prepare(self, batch_size=1, q_len=4096, kv_len=4096, dtype=torch.float16, device="cpu", seed=0):
+        spec = super().prepare(batch_size, q_len, kv_len, dtype, device, seed)
+        g = torch.Generator().manual_seed(seed + 1)
+        spec["input"]["exp_rand"] = _oa.exp_rand(batch_size, self.head_num, q_len, kv_len, g).to(device)
+        return spec
+
+    def forward(self, q, k, v, exp_rand):
+        out, score, _ = _oa.keyformer(q.cpu(), k.cpu(), v.cpu(), exp_rand.cpu(), tau=self.tau)
+        return out, score.view(q.shape[0], self.kv_head_num, k.shape[1])

@@ -1,4 +1,4 @@
-"""GPU parity of the other KV-selection cases of the reference (RoCo, SnapKV, Corm) and of the selection ops
+"""GPU parity of the other KV-selection cases of the reference (RoCo, SnapKV, Corm, KeyFormer) and of the selection ops
 around them (pooling, KV-cache compaction), against the CPU oracle on identical seeded inputs."""
 import numpy as np
 import pytest
@@ -80,6 +80,27 @@ def test_corm_matches_oracle(gpu, S, H, D):
     assert hit0.all()
 
 
+@pytest.mark.parametrize("S,H,D,aligned", [(300, 2, 128, True), (1000, 2, 128, True), (257, 2, 64, True),
+                                            (301, 2, 128, False)])
+def test_keyformer_matches_oracle(gpu, S, H, D, aligned):
+    progress(f"keyformer S{S} H{H} D{D} aligned={aligned}")
+    q, k, v = _qkv(S, H, D, 4 * S + D, sinks=4)
+    g = torch.Generator().manual_seed(S)
+    er = oa.exp_rand(1, H, S, S, g)
+    if aligned:
+        er_dev = er.to(gpu)
+    else:  # rows of S + 1 floats from an offset of one element: the unaligned (4-byte load) path
+        big = torch.ones(1, H, S, S + 2)
+        big[..., 1:S + 1] = er
+        er_dev = big.to(gpu)[..., 1:S + 1]
+    out, score = A.keyformer_attention(q.to(gpu), k.to(gpu), v.to(gpu), er_dev, tau=1.5)
+    ref_out, ref_score, _ = oa.keyformer(q, k, v, er, tau=1.5)
+    what = f"keyformer S{S} H{H} D{D}"
+    assert_close(out.cpu().float(), ref_out.float(), *TOL_F16, what + " out")
+    assert_close(score.cpu(), ref_score, 1e-6, 1e-3, what + " kf_score")
+    assert_close(score.sum(-1).cpu(), torch.full((1, H), float(S)), 0, 1e-4, what + " sum of kf scores = q_len")
+
+
 def test_colscore_thresholds_and_strides(gpu):
     # a strided threshold view and an arbitrary threshold: any(p >= t) with t = 0.05 everywhere
     S, H, D = 200, 2, 128
@@ -119,7 +140,7 @@ def test_avg_pool1d_matches_oracle(gpu):
         assert_close(A.avg_pool1d(x.to(gpu), ks).cpu(), osel.avg_pool1d(x, ks), 1e-6, 1e-6, f"pool k={ks}")
 
 
-@pytest.mark.parametrize("case_cls", [ocases.RoCo, ocases.SnapKV, ocases.Corm])
+@pytest.mark.parametrize("case_cls", [ocases.RoCo, ocases.SnapKV, ocases.Corm, ocases.KeyFormer])
 def test_compile_drop_in_selection_cases(gpu, case_cls):
     # run_kernel.py:44-78 flow for the other selection cases
     model = case_cls(kv_head_num=4, head_num=4, head_dim=128).eval()
@@ -159,3 +180,9 @@ def test_selection_full_size_heads(gpu):
     _, hit = A.corm_attention(qg, kg, vg, thr.to(gpu))
     n = _corm_check(hit, q, k, v, thr, "corm full")
     progress(f"corm full: {n} tie-decided keys")
+    progress("keyformer full size")
+    er = oa.exp_rand(1, H, S, S, torch.Generator().manual_seed(4))
+    _, ref_kf, _ = oa.keyformer(q, k, v, er, q_chunk=512)
+    _, kf = A.keyformer_attention(qg, kg, vg, er.to(gpu))
+    assert_close(kf.cpu(), ref_kf, 1e-6, 1e-3, "kf_score full")
+    np.testing.assert_array_equal(A.topk_indices(kf, 256).cpu().numpy(), osel.topk_indices(ref_kf.numpy(), 256))

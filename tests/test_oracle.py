@@ -277,3 +277,23 @@ def test_kv_gather_matches_loops():
                 assert torch.equal(kv[b, 0, i, h], k[b, j, h]) and torch.equal(kv[b, 1, i, h], v[b, j, h])
     ident = torch.arange(n).view(1, 1, n).expand(B, H, n).contiguous()
     assert torch.equal(osel.kv_gather(k, v, ident)[:, 0], k[:, :n])
+
+
+def test_keyformer_matches_brute_and_invariants():
+    q, k, v = _sel_inputs(9, S=19)
+    er = oa.exp_rand(1, 2, 19, 19, torch.Generator().manual_seed(3))
+    assert (er >= 1).all()
+    out, score, lse2p = oa.keyformer(q, k, v, er, tau=1.5)
+    want = brute.keyformer_colsum(q.tolist(), k.tolist(), er.tolist(), tau=1.5)
+    assert_close(score, torch.tensor(want), 1e-6, 1e-5, "keyformer kf_score vs brute")
+    # every perturbed softmax row sums to 1; the last key is seen by the last query alone
+    assert_close(score.sum(-1), torch.full((1, 2), 19.0), 0, 1e-5, "sum of kf scores = q_len")
+    assert_close(out, oa.attention(q, k, v), 0, 0, "keyformer out == attention")
+    # exp_rand = 1 (gumbels 0) and tau = 1 reduce to the H2O column sums exactly; tau = 2 halves the logits
+    ones = torch.ones_like(er)
+    assert_close(oa.keyformer(q, k, v, ones, tau=1.0)[1], oa.h2o(q, k, v)[1], 0, 0, "kf(e=1, tau=1) == h2o")
+    half = brute.keyformer_colsum((q / 2).tolist(), k.tolist(), ones.tolist(), tau=1.0)
+    assert_close(oa.keyformer(q, k, v, ones, tau=2.0)[1], torch.tensor(half), 1e-6, 1e-5, "tau = 2 == q / 2")
+    # the row lse of the perturbed scores: row 0 sees key 0 only, so lse2p = (s_00 - ln e_00) / tau / ln 2
+    s00 = float((q[0, 0, 0] @ k[0, 0, 0]) / math.sqrt(8))
+    assert abs(float(lse2p[0, 0, 0]) - (s00 - math.log(float(er[0, 0, 0, 0]))) / 1.5 / math.log(2)) < 1e-5

@@ -147,6 +147,14 @@ def bench_variants(args, dev):
                      ("cfg4_corm", lambda: A.corm_attention(q, k, v, thr))):
         ms = statistics.mean(_events_time(fn, 5, 1))
         res[name] = dict(ms=round(ms, 4), tflops=round(cfg.reference_flops() / (ms * 1e-3) / 1e12, 1))
+    # KeyFormer (kf.py): exp_rand [1, 32, 4096, 4096] fp32 (1 + |N(0,1)|, kf.py:48); its causal half is read twice
+    # (row lse pass, column pass)
+    er = 1 + torch.randn(cfg.B, cfg.Hq, cfg.Sq, cfg.Sk, device=dev).abs()
+    ms = statistics.mean(_events_time(lambda: A.keyformer_attention(q, k, v, er), 5, 1))
+    er_bytes = 2 * cfg.B * cfg.Hq * (cfg.Sq * (cfg.Sq + 1) // 2) * 4
+    res["cfg4_keyformer"] = dict(ms=round(ms, 4), tflops=round(cfg.reference_flops() / (ms * 1e-3) / 1e12, 1),
+                                 exp_rand_gbps=round(er_bytes / (ms * 1e-3) / 1e9, 1))
+    del er
     idx = A.topk_indices(A.h2o_attention(q, k, v)[1], cfg.topk)
     ms = statistics.mean(_events_time(lambda: A.kv_gather(k, v, idx), 20, 2))
     nb = 2 * 2 * idx.numel() * cfg.D * k.element_size()  # K and V rows read once and written once

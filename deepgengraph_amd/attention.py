@@ -225,6 +225,24 @@ def kv_gather(k: torch.Tensor, v: torch.Tensor, indices: torch.Tensor) -> torch.
     return out
 
 
+def nonzero(x: torch.Tensor) -> torch.Tensor:
+    """torch.nonzero of a bool / uint8 tensor (Corm's key selection, deepgengraph_exp/cases/models/corm.py:53):
+    int64 [count, x.dim()] coordinates of the nonzero elements in row-major order. Reads the count back to the
+    host (as torch.nonzero does) to size the result."""
+    dev = _lib.require_gpu(x)
+    if x.dtype not in (torch.bool, torch.uint8) or not x.is_contiguous() or x.dim() < 1:
+        raise RuntimeError("nonzero: x must be a contiguous bool / uint8 tensor with at least one dimension")
+    numel = x.numel()
+    n = x.shape[-1]
+    rows = numel // n if n else 0
+    ws = torch.empty(max(int(_lib.load().dgg_nonzero_workspace_bytes(rows)), 8), dtype=torch.uint8, device=x.device)
+    coords = torch.empty(max(numel, 1), x.dim(), dtype=torch.int64, device=x.device)
+    total = torch.empty(1, dtype=torch.int64, device=x.device)
+    _lib.call("dgg_nonzero", _lib.ptr(x), x.dim(), _lib.int64_array(list(x.shape)), _lib.ptr(coords), numel,
+              _lib.ptr(total), _lib.ptr(ws), ws.numel(), _lib.stream_handle(dev))
+    return coords[: int(total.item())]
+
+
 def topk_indices(scores: torch.Tensor, k: int) -> torch.Tensor:
     """deepgengraph_exp/cases/models/h2o.py:51-52 (torch.topk then sort of the indices) with a defined tie
     order: the k largest of each row of scores [..., n] (fp32), ties broken by the lowest index, returned as int64

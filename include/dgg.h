@@ -161,6 +161,15 @@ int dgg_avg_pool1d(const float* in, float* out, int64_t rows, int64_t n, int64_t
 int dgg_kv_gather(const void* k, const void* v, const int64_t* indices, void* out, int64_t B, int64_t S, int64_t Hkv,
                   int64_t D, int64_t n_sel, const int64_t* strides, int dtype, void* stream);
 
+/* Corm's selection of the flagged keys (deepgengraph_exp/cases/models/corm.py:53: torch.nonzero(corm_score)):
+ * the coordinates of the nonzero bytes of a row-major tensor of shape dims[0..ndim), in row-major order, as
+ * coords[i][0..ndim) int64 (the first min(total, max_out) entries are written). *total (device int64, 8-byte
+ * aligned) receives the number of nonzeros. workspace: dgg_nonzero_workspace_bytes(rows) bytes, 8-byte aligned,
+ * rows = numel / dims[ndim-1]. ndim in [1, 8]. Three launches; nothing is allocated. */
+int64_t dgg_nonzero_workspace_bytes(int64_t rows);
+int dgg_nonzero(const uint8_t* in, int ndim, const int64_t* dims, int64_t* coords, int64_t max_out, int64_t* total,
+                void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Top-k of H2O scores (deepgengraph_exp/cases/models/h2o.py:51-52: torch.topk then sort of the indices):
  * for each of `rows` rows of n fp32 scores (row stride n), the k largest, ties broken by the lowest index,
  * written as int64 indices in ascending index order to out_idx [rows, k]. -0.0 equals +0.0; NaN is not

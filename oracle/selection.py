@@ -1,5 +1,5 @@
-"""CPU restatement of the KV-cache selection (top-k, SnapKV pooling, compaction gather) — TEST INFRASTRUCTURE ONLY
-(see oracle/__init__.py)."""
+"""CPU restatement of the KV-cache selection (top-k, SnapKV pooling, compaction gather, Corm's nonzero) — TEST
+INFRASTRUCTURE ONLY (see oracle/__init__.py)."""
 from __future__ import annotations
 
 import numpy as np
@@ -35,3 +35,9 @@ def kv_gather(k: torch.Tensor, v: torch.Tensor, indices: torch.Tensor) -> torch.
     kc = torch.gather(k, dim=1, index=idx).view(B, 1, n, Hkv, D)     # models/h2o.py:54
     vc = torch.gather(v, dim=1, index=idx).view(B, 1, n, Hkv, D)     # models/h2o.py:55
     return torch.cat([kc, vc], dim=1)                                # models/h2o.py:56
+
+
+def nonzero(x: torch.Tensor) -> torch.Tensor:
+    """deepgengraph_exp/cases/models/corm.py:53 (torch.nonzero(corm_score)): int64 [count, x.dim()] coordinates of
+    the nonzero elements in row-major order (the library routine the reference calls, on the CPU)."""
+    return torch.nonzero(x)

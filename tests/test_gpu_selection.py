@@ -134,6 +134,30 @@ def test_kv_gather_matches_oracle(gpu, dtype):
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("shape,density", [((1, 32, 4096), 0.02), ((2, 3, 1000), 0.5), ((5,), 0.6),
+                                           ((3, 2, 2, 300), 1.0), ((4, 700), 0.0), ((3, 0), 0.5)])
+def test_nonzero_matches_oracle(gpu, shape, density):
+    g = torch.Generator().manual_seed(len(shape) * 7 + int(density * 10))
+    x = torch.rand(*shape, generator=g) < density
+    got = A.nonzero(x.to(gpu))
+    want = osel.nonzero(x)
+    assert got.dtype == torch.int64 and got.shape == want.shape, (got.shape, want.shape)
+    assert torch.equal(got.cpu(), want)
+    if x.numel():
+        assert torch.equal(A.nonzero(x.to(torch.uint8).to(gpu)).cpu(), want)  # uint8 input
+
+
+def test_corm_selection_nonzero(gpu):
+    # models/corm.py:45-55: the keys Corm flags, as coordinates (b, h, j) in row-major order
+    S, H, D = 500, 3, 128
+    q, k, v = _qkv(S, H, D, 17, sinks=3)
+    thr = oa.corm_mask(S, S)
+    _, hit = A.corm_attention(q.to(gpu), k.to(gpu), v.to(gpu), thr.to(gpu))
+    sel = A.nonzero(hit)
+    assert torch.equal(sel.cpu(), torch.nonzero(hit.cpu()))
+    assert sel.shape[1] == 3 and (sel[:, 2] == 0).sum().item() == H  # key 0 is flagged in every head
+
+
 def test_avg_pool1d_matches_oracle(gpu):
     x = torch.randn(6, 1000, generator=torch.Generator().manual_seed(2))
     for ks in (1, 3, 5, 9):

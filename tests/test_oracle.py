@@ -297,3 +297,12 @@ def test_keyformer_matches_brute_and_invariants():
     # the row lse of the perturbed scores: row 0 sees key 0 only, so lse2p = (s_00 - ln e_00) / tau / ln 2
     s00 = float((q[0, 0, 0] @ k[0, 0, 0]) / math.sqrt(8))
     assert abs(float(lse2p[0, 0, 0]) - (s00 - math.log(float(er[0, 0, 0, 0]))) / 1.5 / math.log(2)) < 1e-5
+
+
+def test_nonzero_matches_loops():
+    g = torch.Generator().manual_seed(12)
+    x = torch.rand(2, 3, 17, generator=g) < 0.3
+    got = osel.nonzero(x)
+    want = [[b, h, j] for b in range(2) for h in range(3) for j in range(17) if bool(x[b, h, j])]
+    assert got.dtype == torch.int64 and got.tolist() == want
+    assert osel.nonzero(torch.zeros(4, 5, dtype=torch.bool)).shape == (0, 2)

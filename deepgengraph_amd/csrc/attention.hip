@@ -250,7 +250,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D
 
   // Epilogue: full row sum, normalise, store O (4 consecutive head-dim elements per store) and lse.
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  const float inv = 1.0f / l_tot;
+  const float inv = p.Sk == 0 ? 0.f : 1.0f / l_tot;  // no keys at all: o = 0 (an empty P.V), lse = -inf
   if (qi < p.Sq) {
     S* op = static_cast<S*>(p.o) + b * p.o_sb + (int64_t)qi * p.o_ss + h * p.o_sh;
 #pragma unroll
@@ -800,7 +800,7 @@ attn_fwd_dma_kernel(AttnParams p) {
   for (int n = 0; n < NQB; ++n) {
     const int qi = qw0 + 32 * n + r;
     const float l_tot = half_swap_sum(l_part[n][0] + l_part[n][1]);
-    const float inv = 1.0f / l_tot;
+    const float inv = p.Sk == 0 ? 0.f : 1.0f / l_tot;  // no keys at all: o = 0 (an empty P.V), lse = -inf
     if (qi < p.Sq) {
       S* op = static_cast<S*>(p.o) + b * p.o_sb + (int64_t)qi * p.o_ss + h * p.o_sh;
 #pragma unroll
@@ -1384,7 +1384,7 @@ extern "C" int dgg_attn_prefill(const void* q, const void* k, const void* v, voi
   if (int rc = validate_attn("attn_prefill", q, k, B, Sq, Sk, Hq, Hkv, D, strides, 12, scale, softcap, window, dtype))
     return rc;
   if (B == 0 || Sq == 0) return DGG_OK;
-  DGG_REQUIRE(v && o, DGG_ERR_NULL, "attn_prefill: null v/o pointer");
+  DGG_REQUIRE(o && (v || Sk == 0), DGG_ERR_NULL, "attn_prefill: null v/o pointer");
   DGG_REQUIRE(dgg::aligned16(v) && dgg::aligned16(o), DGG_ERR_ALIGN, "attn_prefill: v/o must be 16-byte aligned");
   AttnParams p = make_params(q, k, v, o, B, Sq, Sk, Hq, Hkv, scale, softcap, window, flags);
   p.lse = lse;
@@ -1392,12 +1392,11 @@ extern "C" int dgg_attn_prefill(const void* q, const void* k, const void* v, voi
   p.k_sb = strides[3]; p.k_ss = strides[4]; p.k_sh = strides[5];
   p.v_sb = strides[6]; p.v_ss = strides[7]; p.v_sh = strides[8];
   p.o_sb = strides[9]; p.o_ss = strides[10]; p.o_sh = strides[11];
-  const int64_t bm = D == 128 ? kD128BM : D == 256 ? kD256BM : kBM;
-  p.n_tiles = (int)((Sq + bm - 1) / bm);
   const bool ref = (flags & DGG_ATTN_REF_ROUNDING) != 0;
   hipStream_t st = dgg::as_stream(stream);
-  // Sk == 0 still launches: with no key tiles every row ends fully masked (o NaN, lse -inf), like any
-  // other row that sees no key.
+  // Sk == 0 still launches and writes o = 0 (the reference's P.V over an empty key axis) and lse = -inf.
+  const int64_t bm = D == 128 ? kD128BM : D == 256 ? kD256BM : kBM;
+  p.n_tiles = (int)((Sq + bm - 1) / bm);
   if (dtype == DGG_BF16) {
     if (D == 64) pick_fwd<BF16, 64>(p, ref, st);
     else if (D == 128) pick_fwd<BF16, 128>(p, ref, st);

@@ -99,8 +99,8 @@ int dgg_rotary_embedding_online(const int32_t* positions, void* query, void* key
  *   mask (flags & DGG_ATTN_CAUSAL: key j visible iff j <= i + Sk - Sq; window > 0: also iff
  *   i + Sk - Sq - j < window); p = softmax_j(scores) in fp32; o = p . v.
  * lse (optional, may be NULL): fp32 [B, Hq, Sq] contiguous, natural-log log-sum-exp of the masked
- * scaled scores (base 2 with DGG_ATTN_LSE_BASE2); -inf for a row with no visible key (its o row is NaN, as the reference's softmax of an
- * all -inf row). strides: 12 int64 = q{b,s,h}, k{b,s,h}, v{b,s,h}, o{b,s,h}. */
+ * scaled scores (base 2 with DGG_ATTN_LSE_BASE2); -inf for a row with no visible key (its o row is NaN, as the
+ * reference's softmax of an all -inf row; with Sk == 0, o is 0, the reference's P.V over an empty key axis). strides: 12 int64 = q{b,s,h}, k{b,s,h}, v{b,s,h}, o{b,s,h}. */
 int dgg_attn_prefill(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t Sq,
                      int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides, float scale,
                      float softcap, int64_t window, uint32_t flags, int dtype, void* stream);

@@ -58,6 +58,33 @@ def test_prefill_matches_oracle(gpu, B, Sq, Sk, Hq, Hkv, D, dtype, causal, softc
     assert_close(lse_c[fin], ref_lse[fin], 2e-2, 1e-2, what + " lse")
 
 
+FAST_CASES = [
+    # bf16, head_dim 128, no lse / soft-cap / reference rounding: B, Sq, Sk, Hq, Hkv, causal, window
+    (1, 512, 512, 2, 2, True, 0),
+    (2, 300, 300, 4, 2, True, 0),       # ragged tiles, GQA, 256-row blocks with a partial second block
+    (1, 130, 700, 2, 1, True, 0),       # Sq < Sk: every wave starts mid-sequence
+    (1, 700, 130, 2, 2, True, 0),       # Sq > Sk: waves whose rows see no key (NaN rows)
+    (1, 1000, 1000, 2, 2, True, 200),   # sliding window: masked tiles on both sides
+    (1, 600, 600, 2, 2, False, 100),    # window without causal
+    (1, 257, 383, 2, 2, False, 0),      # non-causal, ragged key tile
+    (3, 64, 64, 1, 1, True, 0),         # one tile, most waves idle
+    (1, 1, 700, 2, 2, True, 0),         # one query row
+    (1, 100, 0, 2, 2, False, 0),        # no keys at all
+]
+
+
+@pytest.mark.parametrize("B,Sq,Sk,Hq,Hkv,causal,window", FAST_CASES)
+def test_prefill_fast_path_matches_oracle(gpu, B, Sq, Sk, Hq, Hkv, causal, window):
+    q, k, v = _qkv(B, Sq, Sk, Hq, Hkv, 128, torch.bfloat16, seed=Sq * 3 + Sk + 11)
+    ref = oa.attention(q, k, v, causal=causal, window=window or None)
+    out = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), causal=causal, window=window)
+    what = f"fast B{B} Sq{Sq} Sk{Sk} H{Hq}/{Hkv} causal={causal} win={window}"
+    got = out.cpu().float()
+    nan = torch.isnan(ref.float())
+    assert torch.equal(torch.isnan(got), nan), what + " NaN rows"
+    assert_close(got[~nan], ref.float()[~nan], *TOL[torch.bfloat16], what)
+
+
 @pytest.mark.parametrize("name,kw,dtype", [
     ("attn_d64_causal_bf16", dict(causal=True), torch.bfloat16),
     ("attn_d64_gqa_softcap_window_bf16", dict(causal=True, softcap=5.0, window=33), torch.bfloat16),

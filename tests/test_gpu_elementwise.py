@@ -28,6 +28,8 @@ def _randn(shape, dtype, seed, scale=1.0, shift=0.0):
     (5, 1001, torch.float16),       # odd width: scalar path
     (3, 65536, torch.bfloat16),     # widest vector path
     (2, 128, torch.bfloat16),
+    (130, 1024, torch.float16),
+    (9, 5120, torch.bfloat16),
 ])
 def test_rms_norm(gpu, rows, hidden, dtype):
     x = _randn((rows, hidden), dtype, 1)
@@ -53,6 +55,11 @@ def test_rms_norm_strided_and_inplace(gpu):
     y = x.clone()
     ops.rms_norm(y, y, w, 1e-5)  # out aliases input
     assert_close(y.cpu().float(), ref.float(), 2e-2, 1e-2, "in-place rms_norm")
+    xw = _randn((6, 2 * 4096), torch.bfloat16, 10).to(gpu)[:, 4096:]  # 4096 wide, strided, in place
+    ww = _randn((4096,), torch.bfloat16, 11, 0.02, 1.0).to(gpu)
+    refw = oe.rms_norm(xw.cpu(), ww.cpu(), 1e-6)
+    ops.rms_norm(xw, xw, ww, 1e-6)
+    assert_close(xw.cpu().float(), refw.float(), 2e-2, 1e-2, "in-place strided rms_norm (4096 wide)")
     x3 = _randn((2, 8, 256), torch.float16, 5).to(gpu)  # leading dims flattened
     o3 = torch.empty_like(x3)
     w3 = torch.ones(256, dtype=torch.float16, device=gpu)

@@ -339,22 +339,27 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 
   const float c = score_coeff<false, REFROUND>(p);
   float m_run = -INFINITY, l_run = 0.f;
-  // element (mb, j) of the S^T accumulators holds key t*BN + mb*32 + 8*(j/4) + 4g + j%4
-  auto tile = [&](int t, int buf, auto masked) {
+  // element (mb, j) of the S^T accumulators holds key t*BN + mb*32 + 8*(j/4) + 4g + j%4. The exp_rand values of
+  // tile t+1 are loaded while tile t is computed (ev_next), so the stream stays in flight under the exp/log work.
+  f32x4 ev[NMB][4], ev_next[NMB][4];
+  auto load_ev = [&](int t, f32x4 (&dst)[NMB][4]) {
     const int kb = t * BN;
-    f32x4 ev[NMB][4];
+    const bool whole = VEC && kb + BN <= p.Sk;  // 16-byte loads: every key of the tile exists
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
       for (int jq = 0; jq < 4; ++jq) {
         const int key = kb + mb * 32 + 8 * jq + 4 * g;
-        if (VEC && !decltype(masked)::value) {
-          ev[mb][jq] = *reinterpret_cast<const f32x4*>(erow + key);
+        if (whole) {
+          dst[mb][jq] = *reinterpret_cast<const f32x4*>(erow + key);
         } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) ev[mb][jq][e] = erow[min(key + e, p.Sk - 1)];
+          for (int e = 0; e < 4; ++e) dst[mb][jq][e] = erow[min(key + e, p.Sk - 1)];
         }
       }
+  };
+  auto tile = [&](int t, int buf, auto masked) {
+    const int kb = t * BN;
     f32x16 sacc[NMB];
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb) sacc[mb] = f32x16{};
@@ -408,16 +413,24 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 
   if (t_begin < t_end) {
     load(t_begin);
+    load_ev(t_begin, ev);
     store(0);
   }
   __syncthreads();
   auto step = [&](int t, auto masked) {
     const int buf = (t - t_begin) & 1;
     const bool more = t + 1 < t_end;
-    if (more) load(t + 1);
+    if (more) {
+      load(t + 1);
+      load_ev(t + 1, ev_next);
+    }
     tile(t, buf, masked);
     if (more) store(buf ^ 1);
     __syncthreads();
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) ev[mb][jq] = ev_next[mb][jq];
   };
   for (int t = t_begin; t < t_full0; ++t) step(t, std::true_type{});
   for (int t = t_full0; t < t_full1; ++t) step(t, std::false_type{});
@@ -1055,6 +1068,7 @@ attn_colsum_d128_kernel(AttnParams p) {
     }
   }
   if (t_full1 * BQ > p.Sq) t_full1 = p.Sq / BQ;  // ragged last tile
+  if (EPI == kColKF && !p.er_lane32) t_full1 = t_full0;  // exp_rand offsets too wide for the full-tile loads
   if (t_full1 < t_full0) t_full1 = t_full0;
 
   // Direct-load lane constants (as the forward's K tiles).
@@ -1097,9 +1111,33 @@ attn_colsum_d128_kernel(AttnParams p) {
   ColAcc<EPI> acc;
   const int kjc = min(kj, p.Sk - 1);
   const float* erp = EPI == kColKF ? p.er + b * p.er_sb + h * p.er_sh : nullptr;  // KeyFormer exp_rand of (b, h)
+  // KeyFormer exp_rand of (row, kjc) for tiles whose rows all exist: a wave-uniform tile address (scalar registers)
+  // plus a 32-bit offset, this lane's part (rows 4g apart, column kjc) plus the row's, one add per load.
+  const uint32_t er_lane_b = EPI == kColKF ? (uint32_t)((4 * g * p.er_ss + kjc) * 4) : 0u;
 
   auto tile = [&](const int t, auto masked) {
     const uint32_t st = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B);
+    float ev[NMB][16];
+    if constexpr (EPI == kColKF) {
+      if constexpr (!decltype(masked)::value) {  // every row of the tile exists (and er_lane32 holds)
+        const char* rb = reinterpret_cast<const char*>(erp + (int64_t)(t * BQ) * p.er_ss);
+        uint32_t ss_b = (uint32_t)(p.er_ss * 4);
+        asm volatile("" : "+s"(ss_b));  // per tile: keeps the 64 offsets from being hoisted into registers
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const uint32_t row_b = (uint32_t)(32 * mb + 8 * (j >> 2) + (j & 3)) * ss_b;
+            ev[mb][j] = *reinterpret_cast<const float*>(rb + (er_lane_b + row_b));
+          }
+      } else {  // rows past the end read the last row (their p is masked)
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            ev[mb][j] = erp[(int64_t)min(t * BQ + 4 * g + 32 * mb + 8 * (j >> 2) + (j & 3), p.Sq - 1) * p.er_ss + kjc];
+      }
+    }
     f32x16 sacc[NMB];
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb) sacc[mb] = f32x16{};
@@ -1133,7 +1171,7 @@ attn_colsum_d128_kernel(AttnParams p) {
         const int o = 32 * mb + 8 * (j >> 2) + (j & 3);
         float pe;
         if constexpr (EPI == kColKF)
-          pe = kf_prob(x * c, erp[(int64_t)min(t * BQ + 4 * g + o, p.Sq - 1) * p.er_ss + kjc], l2, p);
+          pe = kf_prob(x * c, ev[mb][j], l2, p);
         else
           pe = fast_exp2(fmaf(x, c, -l2));
         bool valid = true;
@@ -1473,6 +1511,7 @@ void set_exp_rand(AttnParams& p, const float* er, const int64_t* er_strides, flo
   p.er_sh = er_strides[1];
   p.er_ss = er_strides[2];
   p.kf_inv_tau = 1.0f / tau;
+  p.er_lane32 = (132 * er_strides[2] + p.Sk) * 4 < (1ll << 31) ? 1 : 0;
 }
 }  // namespace
 

@@ -101,6 +101,24 @@ def test_keyformer_matches_oracle(gpu, S, H, D, aligned):
     assert_close(score.sum(-1).cpu(), torch.full((1, H), float(S)), 0, 1e-4, what + " sum of kf scores = q_len")
 
 
+def test_keyformer_wide_exp_rand_rows(gpu):
+    # exp_rand rows 4.1M floats apart: the column pass's 32-bit tile offsets do not fit, every tile takes the
+    # general addressing (a 4.2 GB device buffer of which the [256, 256] corner is used)
+    S, H, D = 256, 1, 128
+    progress("keyformer wide exp_rand rows")
+    q, k, v = _qkv(S, H, D, 77, sinks=2)
+    er = oa.exp_rand(1, H, S, S, torch.Generator().manual_seed(78))
+    wide = 4_100_000
+    buf = torch.empty(S, wide, dtype=torch.float32, device=gpu)
+    buf[:, :S] = er[0, 0].to(gpu)
+    er_dev = buf[:, :S].view(1, 1, S, S)
+    out, score = A.keyformer_attention(q.to(gpu), k.to(gpu), v.to(gpu), er_dev, tau=1.5)
+    ref_out, ref_score, _ = oa.keyformer(q, k, v, er, tau=1.5)
+    assert_close(out.cpu().float(), ref_out.float(), *TOL_F16, "keyformer wide out")
+    assert_close(score.cpu(), ref_score, 1e-6, 1e-3, "keyformer wide kf_score")
+    del buf
+
+
 def test_colscore_thresholds_and_strides(gpu):
     # a strided threshold view and an arbitrary threshold: any(p >= t) with t = 0.05 everywhere
     S, H, D = 200, 2, 128

@@ -16,6 +16,8 @@
 // ragged end of K) evaluate the per-element mask. Workgroups are ordered longest-first and grouped by
 // head inside each XCD (blockIdx round-robins over the 8 XCDs) so the K/V of a head stay in one L2.
 #include <algorithm>
+#include <cstring>
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -29,7 +31,7 @@ using namespace dgg_attn;
 // ------------------------------------------------------------------------------------------------
 // Forward kernel.
 // ------------------------------------------------------------------------------------------------
-template <typename T, int D, int BN, bool MASK, bool SOFTCAP, bool REFROUND>
+template <typename T, int D, int BN, bool MASK, bool SOFTCAP, int REFROUND>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2, 2))) attn_fwd_kernel(AttnParams p) {
   typedef typename T::scalar S;
   typedef typename T::vec8 V8;
@@ -280,7 +282,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D
 // query per lane, so the row reduction stays in the lane (plus one cross-half step). K tiles of 64 keys are staged
 // through double-buffered LDS; exp_rand is read once, as 16-byte loads when VEC (rows 16-byte aligned).
 // ------------------------------------------------------------------------------------------------
-template <typename T, int D, bool MASK, bool REFROUND, bool VEC>
+template <typename T, int D, bool MASK, int REFROUND, bool VEC>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_kf_rowlse_kernel(AttnParams p) {
   typedef typename T::scalar S;
   typedef typename T::vec8 V8;
@@ -444,7 +446,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 // per tile; NSTAGE: tiles in the LDS ring; OCC: waves per SIMD the register budget is sized for. FASTSUM: the row
 // sums add the 16-bit rounded probabilities two at a time (v_dot2); used when no lse is written, since the O
 // normalisation tolerates the rounding but the column-sum pass needs the fp32 row sums.
-template <typename T, int D, int NQB, int NW, int BN, int NSTAGE, int OCC, bool MASK, bool SOFTCAP, bool REFROUND,
+template <typename T, int D, int NQB, int NW, int BN, int NSTAGE, int OCC, bool MASK, bool SOFTCAP, int REFROUND,
           bool FASTSUM>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 attn_fwd_dma_kernel(AttnParams p) {
@@ -677,7 +679,7 @@ attn_fwd_dma_kernel(AttnParams p) {
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
-          for (int jp = 0; jp < 8; ++jp) hs[n][mb][jp] = ref_scores_f16(sacc[n][mb][2 * jp], sacc[n][mb][2 * jp + 1], p);
+          for (int jp = 0; jp < 8; ++jp) hs[n][mb][jp] = ref_scores_f16<REFROUND>(sacc[n][mb][2 * jp], sacc[n][mb][2 * jp + 1], p);
       }
       if constexpr (PKM) {
         f16x2 mx = hs[n][0][0];
@@ -842,7 +844,7 @@ attn_fwd_dma_kernel(AttnParams p) {
 constexpr int kCBQ = 64;   // query rows per tile
 constexpr int kCBK = 32 * kWaves;  // keys per workgroup
 
-template <typename T, int D, bool MASK, bool SOFTCAP, bool REFROUND, int EPI>
+template <typename T, int D, bool MASK, bool SOFTCAP, int REFROUND, int EPI>
 __global__ void __launch_bounds__(kThreads) attn_colsum_kernel(AttnParams p) {
   typedef typename T::scalar S;
   typedef typename T::vec8 V8;
@@ -995,7 +997,7 @@ __device__ __forceinline__ void dma4(uint32_t lds, const void* vaddr) {
                : "memory", "m0");
 }
 
-template <typename T, int NW, int BQ, int NSTAGE, bool MASK, bool SOFTCAP, bool REFROUND, bool LSE2, int EPI>
+template <typename T, int NW, int BQ, int NSTAGE, bool MASK, bool SOFTCAP, int REFROUND, bool LSE2, int EPI>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_colsum_d128_kernel(AttnParams p) {
   constexpr int D = 128;
@@ -1160,7 +1162,7 @@ attn_colsum_d128_kernel(AttnParams p) {
       f16x2 hs[8];
       if constexpr (PK) {
 #pragma unroll
-        for (int jp = 0; jp < 8; ++jp) hs[jp] = ref_scores_f16(sacc[mb][2 * jp], sacc[mb][2 * jp + 1], p);
+        for (int jp = 0; jp < 8; ++jp) hs[jp] = ref_scores_f16<REFROUND>(sacc[mb][2 * jp], sacc[mb][2 * jp + 1], p);
       }
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
@@ -1215,13 +1217,13 @@ attn_colsum_d128_kernel(AttnParams p) {
   acc.store(p, bh, kj, g);
 }
 
-template <typename T, int D, int BN, bool MASK, bool SOFTCAP, bool REFROUND>
+template <typename T, int D, int BN, bool MASK, bool SOFTCAP, int REFROUND>
 void launch_fwd(const AttnParams& p, hipStream_t st) {
   const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
   hipLaunchKernelGGL((attn_fwd_kernel<T, D, BN, MASK, SOFTCAP, REFROUND>), dim3(grid), dim3(kThreads), 0, st, p);
 }
 
-template <typename T, int D, bool MASK, bool SOFTCAP, bool REFROUND, int EPI>
+template <typename T, int D, bool MASK, bool SOFTCAP, int REFROUND, int EPI>
 void launch_colsum(const AttnParams& p, hipStream_t st) {
   const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
   hipLaunchKernelGGL((attn_colsum_kernel<T, D, MASK, SOFTCAP, REFROUND, EPI>), dim3(grid), dim3(kThreads), 0, st, p);
@@ -1231,7 +1233,7 @@ void launch_colsum(const AttnParams& p, hipStream_t st) {
 constexpr int kD128NQB = 1, kD128NW = 8, kD128BN = 128, kD128NS = 2;
 constexpr int kD128BM = 32 * kD128NQB * kD128NW;  // query rows per workgroup (head_dim 128)
 
-template <typename T, bool MASK, bool SOFTCAP, bool REFROUND>
+template <typename T, bool MASK, bool SOFTCAP, int REFROUND>
 void launch_fwd_d128(const AttnParams& p, hipStream_t st) {
   const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
   if (!REFROUND && p.lse == nullptr)
@@ -1251,7 +1253,7 @@ void launch_fwd_d128(const AttnParams& p, hipStream_t st) {
 constexpr int kD256NW = 4, kD256BN = DGG_D256_BN, kD256NS = 2;
 constexpr int kD256BM = 32 * kD256NW;
 
-template <typename T, bool MASK, bool SOFTCAP, bool REFROUND>
+template <typename T, bool MASK, bool SOFTCAP, int REFROUND>
 void launch_fwd_d256(const AttnParams& p, hipStream_t st) {
   const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
   if (!REFROUND && p.lse == nullptr)
@@ -1262,19 +1264,33 @@ void launch_fwd_d256(const AttnParams& p, hipStream_t st) {
                        dim3(grid), dim3(64 * kD256NW), 0, st, p);
 }
 
+// Reference-rounding mode of a launch (the REFROUND template argument): 0 off, 1 the exact fp32 division
+// sequence (ref_quot), 2 one multiply by the host-verified ref_mul. Mode 2 is built for head_dim 128 without
+// soft-cap (the config-4 family: H2O, RoCo, SnapKV, Corm, KeyFormer); everything else uses mode 1.
+template <int D, bool SOFTCAP, typename F>
+void with_ref_mode(bool ref, const AttnParams& p, F&& f) {
+  if (!ref) {
+    f(std::integral_constant<int, 0>{});
+    return;
+  }
+  if constexpr (D == 128 && !SOFTCAP) {
+    if (p.ref_mul_ok) {
+      f(std::integral_constant<int, 2>{});
+      return;
+    }
+  }
+  f(std::integral_constant<int, 1>{});
+}
+
 template <typename T, int D, bool MASK, bool SOFTCAP>
 void pick_fwd_ref(const AttnParams& p, bool ref, hipStream_t st) {
   constexpr int BN = D >= 256 ? 32 : 64;
-  if constexpr (D == 128) {
-    if (ref) launch_fwd_d128<T, MASK, SOFTCAP, true>(p, st);
-    else launch_fwd_d128<T, MASK, SOFTCAP, false>(p, st);
-  } else if constexpr (D == 256) {
-    if (ref) launch_fwd_d256<T, MASK, SOFTCAP, true>(p, st);
-    else launch_fwd_d256<T, MASK, SOFTCAP, false>(p, st);
-  } else {
-    if (ref) launch_fwd<T, D, BN, MASK, SOFTCAP, true>(p, st);
-    else launch_fwd<T, D, BN, MASK, SOFTCAP, false>(p, st);
-  }
+  with_ref_mode<D, SOFTCAP>(ref, p, [&](auto mode) {
+    constexpr int R = decltype(mode)::value;
+    if constexpr (D == 128) launch_fwd_d128<T, MASK, SOFTCAP, R>(p, st);
+    else if constexpr (D == 256) launch_fwd_d256<T, MASK, SOFTCAP, R>(p, st);
+    else launch_fwd<T, D, BN, MASK, SOFTCAP, R>(p, st);
+  });
 }
 template <typename T, int D>
 void pick_fwd(const AttnParams& p, bool ref, hipStream_t st) {
@@ -1292,7 +1308,7 @@ void pick_fwd(const AttnParams& p, bool ref, hipStream_t st) {
 constexpr int kC128NW = 8, kC128BQ = 128, kC128NS = 2;
 constexpr int kC128BK = 32 * kC128NW;  // keys per workgroup (head_dim 128)
 
-template <typename T, bool MASK, bool SOFTCAP, bool REFROUND, int EPI>
+template <typename T, bool MASK, bool SOFTCAP, int REFROUND, int EPI>
 void launch_colsum_d128(const AttnParams& p, hipStream_t st) {
   const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
   if (p.lse_base2)
@@ -1303,22 +1319,22 @@ void launch_colsum_d128(const AttnParams& p, hipStream_t st) {
                        dim3(grid), dim3(64 * kC128NW), 0, st, p);
 }
 
-template <typename T, int D, bool MASK, bool SOFTCAP, bool REFROUND, int EPI>
+template <typename T, int D, bool MASK, bool SOFTCAP, int REFROUND, int EPI>
 void launch_col(const AttnParams& p, hipStream_t st) {
   if constexpr (D == 128) launch_colsum_d128<T, MASK, SOFTCAP, REFROUND, EPI>(p, st);
   else launch_colsum<T, D, MASK, SOFTCAP, REFROUND, EPI>(p, st);
 }
 template <typename T, int D, bool MASK, bool SOFTCAP>
 void pick_col_ref(const AttnParams& p, bool ref, hipStream_t st) {
-  if (ref) launch_col<T, D, MASK, SOFTCAP, true, kColSum>(p, st);
-  else launch_col<T, D, MASK, SOFTCAP, false, kColSum>(p, st);
+  with_ref_mode<D, SOFTCAP>(ref, p, [&](auto mode) {
+    launch_col<T, D, MASK, SOFTCAP, decltype(mode)::value, kColSum>(p, st);
+  });
 }
 // The RoCo / Corm epilogues exist for the mask-checking, soft-cap-free variants only (the reference cases are
 // causal and have no soft-cap); the host rejects a soft-cap with them.
 template <typename T, int D, int EPI>
 void pick_col_epi(const AttnParams& p, bool ref, hipStream_t st) {
-  if (ref) launch_col<T, D, true, false, true, EPI>(p, st);
-  else launch_col<T, D, true, false, false, EPI>(p, st);
+  with_ref_mode<D, false>(ref, p, [&](auto mode) { launch_col<T, D, true, false, decltype(mode)::value, EPI>(p, st); });
 }
 template <typename T, int D>
 void pick_col(const AttnParams& p, bool ref, int epi, hipStream_t st) {
@@ -1336,7 +1352,7 @@ void pick_col(const AttnParams& p, bool ref, int epi, hipStream_t st) {
   }
 }
 
-template <typename T, int D, bool MASK, bool REFROUND>
+template <typename T, int D, bool MASK, int REFROUND>
 void launch_kf_rowlse(const AttnParams& p, bool vec, hipStream_t st) {
   const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
   if (vec) hipLaunchKernelGGL((attn_kf_rowlse_kernel<T, D, MASK, REFROUND, true>), dim3(grid), dim3(kThreads), 0, st, p);
@@ -1345,13 +1361,11 @@ void launch_kf_rowlse(const AttnParams& p, bool vec, hipStream_t st) {
 template <typename T, int D>
 void pick_kf_rowlse(const AttnParams& p, bool ref, bool vec, hipStream_t st) {
   const bool mask = p.causal || p.window > 0;
-  if (mask) {
-    if (ref) launch_kf_rowlse<T, D, true, true>(p, vec, st);
-    else launch_kf_rowlse<T, D, true, false>(p, vec, st);
-  } else {
-    if (ref) launch_kf_rowlse<T, D, false, true>(p, vec, st);
-    else launch_kf_rowlse<T, D, false, false>(p, vec, st);
-  }
+  with_ref_mode<D, false>(ref, p, [&](auto mode) {
+    constexpr int R = decltype(mode)::value;
+    if (mask) launch_kf_rowlse<T, D, true, R>(p, vec, st);
+    else launch_kf_rowlse<T, D, false, R>(p, vec, st);
+  });
 }
 
 // Shared host-side validation of the attention arguments.
@@ -1386,6 +1400,110 @@ int validate_attn(const char* op, const void* q, const void* k, int64_t B, int64
   return DGG_OK;
 }
 
+// 16-bit rounding (to nearest even, overflow to infinity) of an fp32 value, as bit patterns.
+uint16_t rn_f16_bits(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);   // NaN
+  if (ax >= 0x47800000u) return (uint16_t)(sign | 0x7c00u);  // >= 2^16 (and inf): infinity
+  if (ax < 0x38800000u) {                                     // below 2^-14: subnormal result in units of 2^-24
+    float a;
+    std::memcpy(&a, &ax, 4);
+    return (uint16_t)(sign | (uint32_t)std::nearbyint(a * 16777216.0f));
+  }
+  uint32_t h = ((((ax >> 23) - 112u) << 10) | ((ax & 0x7fffffu) >> 13));
+  const uint32_t rem = ax & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;  // a carry moves into the exponent (65520.. -> inf)
+  return (uint16_t)(sign | h);
+}
+uint16_t rn_bf16_bits(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+  return (uint16_t)((x + 0x7fffu + ((x >> 16) & 1u)) >> 16);
+}
+float f16_bits_value(uint16_t h) {
+  const int e = (h >> 10) & 31, m = h & 1023;
+  const float mag = e == 0 ? std::ldexp((float)m, -24) : e == 31 ? (m ? NAN : INFINITY) : std::ldexp((float)(1024 + m), e - 25);
+  return (h & 0x8000u) ? -mag : mag;
+}
+
+// The reference divides each 16-bit score x by d in fp32 and rounds the quotient back to 16 bits
+// (attn.py:29, h2o.py:29). Looks for an fp32 multiplier y with RN16(RN32(x * y)) == RN16(RN32(x / d)) for every
+// finite 16-bit x (signed zeros equal), trying RN(1/d) and then the fp32 values up to 4 ulps around it; the
+// kernels then replace the division sequence by one multiply (reference-rounding mode 2). The exhaustive check
+// runs once per (dtype, d); results are cached.
+bool ref_multiplier(int dtype, float d, float* y_out) {
+  struct Entry {
+    int dtype;
+    uint32_t dbits;
+    bool ok;
+    float y;
+  };
+  static std::mutex mu;
+  static Entry cache[32];
+  static int n_cache = 0;
+  uint32_t dbits;
+  std::memcpy(&dbits, &d, 4);
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < n_cache; ++i)
+      if (cache[i].dtype == dtype && cache[i].dbits == dbits) {
+        *y_out = cache[i].y;
+        return cache[i].ok;
+      }
+  }
+  const bool f16 = dtype == DGG_F16;
+  auto rn = [&](float v) { return f16 ? rn_f16_bits(v) : rn_bf16_bits(v); };
+  auto works = [&](float y) {
+    for (uint32_t b = 0; b < 65536u; ++b) {
+      float x;
+      if (f16) {
+        x = f16_bits_value((uint16_t)b);
+      } else {
+        const uint32_t xb = b << 16;
+        std::memcpy(&x, &xb, 4);
+      }
+      if (!std::isfinite(x)) continue;
+      const uint16_t want = rn(x / d), got = rn(x * y);
+      if (want != got && ((want | got) & 0x7fffu) != 0) return false;
+    }
+    return true;
+  };
+  const float y0 = 1.0f / d;
+  float cand[9] = {y0};
+  float up = y0, down = y0;
+  for (int i = 1; i <= 4; ++i) {
+    up = std::nextafter(up, INFINITY);
+    down = std::nextafter(down, 0.0f);
+    cand[2 * i - 1] = up;
+    cand[2 * i] = down;
+  }
+  bool ok = false;
+  float y = y0;
+  if (std::isfinite(d) && d > 0.f && std::isfinite(y0) && y0 > 0.f)
+    for (float c : cand)
+      if (works(c)) {
+        ok = true;
+        y = c;
+        break;
+      }
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    if (n_cache < 32) cache[n_cache++] = Entry{dtype, dbits, ok, y};
+  }
+  *y_out = y;
+  return ok;
+}
+
+// Reference-rounding parameters of a launch: the verified multiplier when reference rounding is on.
+void set_ref_mode(AttnParams& p, uint32_t flags, int dtype) {
+  p.ref_mul = p.ref_rcp;
+  p.ref_mul_ok = 0;
+  if (flags & DGG_ATTN_REF_ROUNDING) p.ref_mul_ok = ref_multiplier(dtype, p.ref_div, &p.ref_mul) ? 1 : 0;
+}
+
 AttnParams make_params(const void* q, const void* k, const void* v, void* o, int64_t B, int64_t Sq, int64_t Sk,
                        int64_t Hq, int64_t Hkv, float scale, float softcap, int64_t window, uint32_t flags) {
   AttnParams p{};
@@ -1416,6 +1534,13 @@ AttnParams make_params(const void* q, const void* k, const void* v, void* o, int
 
 }  // namespace
 
+extern "C" int dgg_ref_multiplier(int dtype, float d, float* y) {
+  DGG_REQUIRE(dtype == DGG_F16 || dtype == DGG_BF16, DGG_ERR_DTYPE, "ref_multiplier: dtype code %d not f16/bf16",
+              dtype);
+  DGG_REQUIRE(y != nullptr, DGG_ERR_NULL, "ref_multiplier: null output pointer");
+  return ref_multiplier(dtype, d, y) ? 1 : 0;
+}
+
 extern "C" int dgg_attn_prefill(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B,
                                 int64_t Sq, int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides,
                                 float scale, float softcap, int64_t window, uint32_t flags, int dtype, void* stream) {
@@ -1425,6 +1550,7 @@ extern "C" int dgg_attn_prefill(const void* q, const void* k, const void* v, voi
   DGG_REQUIRE(o && (v || Sk == 0), DGG_ERR_NULL, "attn_prefill: null v/o pointer");
   DGG_REQUIRE(dgg::aligned16(v) && dgg::aligned16(o), DGG_ERR_ALIGN, "attn_prefill: v/o must be 16-byte aligned");
   AttnParams p = make_params(q, k, v, o, B, Sq, Sk, Hq, Hkv, scale, softcap, window, flags);
+  set_ref_mode(p, flags, dtype);
   p.lse = lse;
   p.q_sb = strides[0]; p.q_ss = strides[1]; p.q_sh = strides[2];
   p.k_sb = strides[3]; p.k_ss = strides[4]; p.k_sh = strides[5];
@@ -1468,6 +1594,7 @@ int colscore(const char* op, const void* q, const void* k, const float* lse, int
   }
   DGG_REQUIRE(Sq == 0 || lse != nullptr, DGG_ERR_NULL, "%s: null lse pointer", op);
   AttnParams p = make_params(q, k, nullptr, nullptr, B, Sq, Sk, Hq, Hkv, scale, softcap, window, flags);
+  set_ref_mode(p, flags, dtype);
   p.lse = const_cast<float*>(lse);
   p.colsum = out0;
   p.colsum2 = out1;
@@ -1526,6 +1653,7 @@ extern "C" int dgg_attn_kf_rowlse(const void* q, const void* k, const float* exp
   DGG_REQUIRE(Sk > 0, DGG_ERR_SHAPE, "%s: Sk must be > 0", op);
   if (int rc = validate_exp_rand(op, exp_rand, er_strides, Sq, tau)) return rc;
   AttnParams p = make_params(q, k, nullptr, nullptr, B, Sq, Sk, Hq, Hkv, scale, 0.f, window, flags);
+  set_ref_mode(p, flags, dtype);
   p.lse = lse2;
   p.q_sb = strides[0]; p.q_ss = strides[1]; p.q_sh = strides[2];
   p.k_sb = strides[3]; p.k_ss = strides[4]; p.k_sh = strides[5];
@@ -1560,6 +1688,7 @@ extern "C" int dgg_attn_kf_colsum(const void* q, const void* k, const float* exp
   // The row lse of the perturbed scores is base 2 (as dgg_attn_kf_rowlse writes it).
   AttnParams p = make_params(q, k, nullptr, nullptr, B, Sq, Sk, Hq, Hkv, scale, 0.f, window,
                              flags | DGG_ATTN_LSE_BASE2);
+  set_ref_mode(p, flags, dtype);
   p.lse = const_cast<float*>(lse2);
   p.colsum = kf_score;
   p.q_sb = strides[0]; p.q_ss = strides[1]; p.q_sh = strides[2];

@@ -45,6 +45,8 @@ struct AttnParams {
   float ref_div;  // 1 / scale rounded to fp32 (== fp32 sqrt(D) for the usual scale): the reference divides
                   // the rounded scores by it
   float ref_rcp;  // 1 / ref_div rounded to fp32
+  float ref_mul;  // fp32 multiplier with RN16(x * ref_mul) == RN16(x / ref_div) for every finite 16-bit x
+  int ref_mul_ok; // ref_mul verified on the host for this dtype (reference rounding mode 2)
   float c_fast;  // scale * log2(e): converts raw scores to the exp2 domain
   float inv_softcap;
   float softcap;
@@ -101,13 +103,15 @@ __device__ __forceinline__ float ref_quot(float x, float d, float y) {
 // row maximum / lse is subtracted and `c` applied) is the unnormalised probability:
 //   fast path (no soft-cap, no reference rounding): the raw fp32 score; the caller multiplies by c_fast.
 //   otherwise: the score already in the exp2 domain (c = 1).
-template <typename T, bool SOFTCAP, bool REFROUND>
+// REFROUND: 0 off; 1 the division by ref_div as the exact sequence above; 2 one multiply by ref_mul, which the host
+// verified to give the same 16-bit result for every finite 16-bit input.
+template <typename T, bool SOFTCAP, int REFROUND>
 __device__ __forceinline__ float score_value(float s, const AttnParams& p) {
   if constexpr (REFROUND) {
     // deepgengraph_exp/cases/kernels/attn.py:29 / gemma2.py:29-33: each step rounded to the input dtype;
     // `/ math.sqrt(D)` is an fp32 true division before the rounding.
     s = round_t<T>(s);
-    s = round_t<T>(ref_quot(s, p.ref_div, p.ref_rcp));
+    s = round_t<T>(REFROUND == 2 ? fmaf(s, p.ref_mul, 0.0f) : ref_quot(s, p.ref_div, p.ref_rcp));
     if constexpr (SOFTCAP) {
       s = round_t<T>(ref_quot(s, p.softcap, p.inv_softcap));
       s = round_t<T>(tanhf(s));
@@ -123,7 +127,7 @@ __device__ __forceinline__ float score_value(float s, const AttnParams& p) {
   }
 }
 
-template <bool SOFTCAP, bool REFROUND>
+template <bool SOFTCAP, int REFROUND>
 __device__ __forceinline__ float score_coeff(const AttnParams& p) {
   return (SOFTCAP || REFROUND) ? 1.0f : p.c_fast;
 }
@@ -164,11 +168,13 @@ struct ColAcc {
 
 // Reference-rounded fp16 scores of two raw fp32 dot products, kept packed (natural-log domain): the matmul
 // output rounded to fp16, divided by ref_div, rounded again (attn.py:29 / h2o.py:29). The conversions are
-// v_cvt_pk_f16_f32 and the fp16 operands feed v_fma_mix_f32 directly, so the pair costs ten instructions.
+// v_cvt_pk_f16_f32 and the fp16 operands feed v_fma_mix_f32 directly, so the pair costs ten instructions with
+// the division sequence (REFROUND 1) and four with the verified multiplier (REFROUND 2).
+template <int REFROUND>
 __device__ __forceinline__ f16x2 ref_scores_f16(float a, float b, const AttnParams& p) {
   const f16x2 h = __builtin_convertvector(f32x2{a, b}, f16x2);
-  const float q0 = ref_quot((float)h[0], p.ref_div, p.ref_rcp);
-  const float q1 = ref_quot((float)h[1], p.ref_div, p.ref_rcp);
+  const float q0 = REFROUND == 2 ? fmaf((float)h[0], p.ref_mul, 0.0f) : ref_quot((float)h[0], p.ref_div, p.ref_rcp);
+  const float q1 = REFROUND == 2 ? fmaf((float)h[1], p.ref_mul, 0.0f) : ref_quot((float)h[1], p.ref_div, p.ref_rcp);
   return __builtin_convertvector(f32x2{q0, q1}, f16x2);
 }
 

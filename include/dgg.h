@@ -170,6 +170,14 @@ int64_t dgg_nonzero_workspace_bytes(int64_t rows);
 int dgg_nonzero(const uint8_t* in, int ndim, const int64_t* dims, int64_t* coords, int64_t max_out, int64_t* total,
                 void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Host-side check behind DGG_ATTN_REF_ROUNDING (no counterpart in the reference: the reference divides in fp32,
+ * attn.py:29). Writes to *y an fp32 multiplier with RN16(RN32(x * y)) == RN16(RN32(x / d)) for every finite
+ * 16-bit x of dtype (f16 or bf16; signed zeros equal) and returns 1, trying RN(1/d) and the 8 fp32 values
+ * nearest it; returns 0 (and *y = RN(1/d)) when none qualifies. The attention entry points call it for
+ * d = 1/scale and, when it succeeds at head_dim 128 without soft-cap, round scores with one multiply instead of
+ * the division sequence. The result is cached per (dtype, d); the first call costs a few milliseconds. */
+int dgg_ref_multiplier(int dtype, float d, float* y);
+
 /* Top-k of H2O scores (deepgengraph_exp/cases/models/h2o.py:51-52: torch.topk then sort of the indices):
  * for each of `rows` rows of n fp32 scores (row stride n), the k largest, ties broken by the lowest index,
  * written as int64 indices in ascending index order to out_idx [rows, k]. -0.0 equals +0.0; NaN is not

@@ -92,3 +92,58 @@ def test_infinite_scores_stay_infinite(ref_quot):
     got = ref_quot(x, np.float32(11.313708))
     assert got[0] == np.inf and got[1] == -np.inf
     np.testing.assert_array_equal(got[2:], (x[2:] / np.float32(11.313708)).astype(np.float32))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from deepgengraph_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        from deepgengraph_amd import build
+
+        build.build()
+    return _lib.load()
+
+
+def _multiplier(lib, dtype, d):
+    import ctypes
+
+    from deepgengraph_amd import _lib
+
+    y = ctypes.c_float(0.0)
+    rc = lib.dgg_ref_multiplier(_lib.dtype_code(dtype), float(d), ctypes.byref(y))
+    assert rc in (0, 1), rc
+    return rc == 1, np.float32(y.value)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_library_multiplier_rounds_like_true_division(lib, dtype):
+    """dgg_ref_multiplier (the host search behind reference-rounding mode 2): whenever it reports a multiplier y,
+    RN16(RN32(x * y)) must equal RN16(RN32(x / d)) for every finite 16-bit x, checked here independently with
+    numpy's IEEE fp32 arithmetic and torch's rounding."""
+    x = _all_values(dtype)
+    found = 0
+    for d in _divisors():
+        ok, y = _multiplier(lib, dtype, d)
+        if not ok:
+            continue
+        found += 1
+        with np.errstate(over="ignore"):
+            got = _round((x * y).astype(np.float32), dtype)
+            want = _round((x / d).astype(np.float32), dtype)
+        assert np.array_equal(got, want, equal_nan=True), f"multiplier {y!r} for d={d!r} is not exact"
+    assert found >= len(_divisors()) // 2
+
+
+def test_library_multiplier_needs_the_search(lib):
+    """fp16, D = 128: RN(1/sqrt(128)) itself changes 52 of the rounded quotients, the next fp32 value up none;
+    the search must return the latter (a plain reciprocal would break reference rounding)."""
+    d = np.float32(1.0 / float(np.float32(1.0 / np.sqrt(128.0))))
+    x = _all_values(torch.float16)
+    y0 = np.float32(1.0) / d
+    want = _round((x / d).astype(np.float32), torch.float16)
+    assert np.count_nonzero(_round((x * y0).astype(np.float32), torch.float16) != want) == 52
+    ok, y = _multiplier(lib, torch.float16, d)
+    assert ok and y == np.nextafter(y0, np.float32(1.0))
+    ok2, y2 = _multiplier(lib, torch.float16, np.float32(8.0))  # D = 64: the reciprocal is exact
+    assert ok2 and y2 == np.float32(0.125)

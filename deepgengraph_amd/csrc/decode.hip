@@ -14,7 +14,10 @@
 namespace {
 
 constexpr int kDecThreads = 256;
-constexpr int kUnroll = 8;  // key rows per lane group per block (loads in flight per lane: 2 * kUnroll)
+#ifndef DGG_DEC_UNROLL
+#define DGG_DEC_UNROLL 8
+#endif
+constexpr int kUnroll = DGG_DEC_UNROLL;  // key rows per lane group per block (loads in flight per lane: 2 * kUnroll)
 
 struct DecodeParams {
   const void* q;
@@ -67,8 +70,9 @@ __global__ void __launch_bounds__(kDecThreads) decode_partial_kernel(DecodeParam
       const int key = base + u * GROUPS + grp;
       ok[u] = key < k1;
       const int kc = min(key, k1 - 1);
-      kr[u] = ld16<V8>(kp + (int64_t)kc * p.k_sl);
-      vr[u] = ld16<V8>(vp + (int64_t)kc * p.v_sl);
+      // non-temporal: each cache row is read once (5.55 -> 5.33 ms at config 5)
+      kr[u] = __builtin_nontemporal_load(reinterpret_cast<const V8*>(kp + (int64_t)kc * p.k_sl));
+      vr[u] = __builtin_nontemporal_load(reinterpret_cast<const V8*>(vp + (int64_t)kc * p.v_sl));
     }
     float s[kUnroll];
     float bm = -INFINITY;

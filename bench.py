@@ -130,7 +130,7 @@ def bench_variants(args, dev):
     cfg = C.CFG3
     q, k, v, _ = C.attn_inputs(cfg, device=dev)
     ms = statistics.mean(_events_time(
-        lambda: A.attention(q, k, v, causal=True, softcap=cfg.softcap, window=cfg.window), 5, 1))
+        lambda: A.attention(q, k, v, causal=True, softcap=cfg.softcap, window=cfg.window), 10, 3))
     res["cfg3_gemma2"] = dict(ms=round(ms, 4), tflops=round(cfg.flops() / (ms * 1e-3) / 1e12, 1),
                               frac=round(cfg.flops() / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))
     del q, k, v

@@ -1140,51 +1140,15 @@ attn_colsum_d128_kernel(AttnParams p) {
             ev[mb][j] = erp[(int64_t)min(t * BQ + 4 * g + 32 * mb + 8 * (j >> 2) + (j & 3), p.Sq - 1) * p.er_ss + kjc];
       }
     }
-    constexpr bool MASKED = decltype(masked)::value;
-    // Masked tiles: per 32-row block, whether no (row, key) pair of the wave is visible (dead: no MFMAs, p = 0)
-    // or every pair is visible with every row < Sq (full: no per-element test). Only the blocks the diagonal or
-    // the window edge crosses, and the ragged last block, are tested element by element.
-    bool blk_dead[NMB], blk_full[NMB];
-#pragma unroll
-    for (int mb = 0; mb < NMB; ++mb) blk_dead[mb] = blk_full[mb] = false;
-    if constexpr (MASKED) {
-#pragma unroll
-      for (int mb = 0; mb < NMB; ++mb) {
-        const int r0 = t * BQ + 32 * mb;  // rows r0 .. r0+31, keys kw0 .. kw0+31
-        bool dead = r0 >= p.Sq, full = r0 + 31 < p.Sq;
-        if constexpr (MASK) {
-          if (p.causal) {
-            dead = dead || kw0 > r0 + 31 + p.offset;
-            full = full && kw0 + 31 <= r0 + p.offset;
-          }
-          if (p.window > 0) {
-            dead = dead || r0 + p.offset - (kw0 + 31) >= p.window;
-            full = full && r0 + 31 + p.offset - kw0 < p.window;
-          }
-        }
-        blk_dead[mb] = dead;
-        blk_full[mb] = full && !dead;
-      }
-    }
     f32x16 sacc[NMB];
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb) sacc[mb] = f32x16{};
-    if constexpr (MASKED) {
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
 #pragma unroll
       for (int mb = 0; mb < NMB; ++mb) {
-        if (blk_dead[mb]) continue;
-#pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk)
-          sacc[mb] = mfma32(lds_read<V8>(st + xq[kk >> 1] + mb * 8 * GROUP_B + 32 * (kk & 1)), kf[kk], sacc[mb]);
-      }
-    } else {
-#pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk) {
-#pragma unroll
-        for (int mb = 0; mb < NMB; ++mb) {
-          const V8 a = lds_read<V8>(st + xq[kk >> 1] + mb * 8 * GROUP_B + 32 * (kk & 1));
-          sacc[mb] = mfma32(a, kf[kk], sacc[mb]);
-        }
+        const V8 a = lds_read<V8>(st + xq[kk >> 1] + mb * 8 * GROUP_B + 32 * (kk & 1));
+        sacc[mb] = mfma32(a, kf[kk], sacc[mb]);
       }
     }
     // Visibility of (row o of the tile, this lane's key): causal rel >= 0, window rel < window, row < Sq.
@@ -1192,19 +1156,6 @@ attn_colsum_d128_kernel(AttnParams p) {
     const int rows_left = p.Sq - t * BQ - 4 * g;
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb) {
-      if (MASKED && blk_dead[mb]) {
-        // p = 0 for the whole block: nothing to add, except that Corm's any(p >= threshold) still compares the
-        // zeros with the thresholds of the rows < Sq, as the reference compares its full probability matrix
-        if constexpr (EPI == kColAnyGe) {
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int o = 32 * mb + 8 * (j >> 2) + (j & 3);
-            acc.add(0.f, o < rows_left, min(t * BQ + 4 * g + o, p.Sq - 1), kjc, p);
-          }
-        }
-        continue;
-      }
-      const bool per_elem = MASKED && !blk_full[mb];
       f32x4 lv[4];
 #pragma unroll
       for (int jq = 0; jq < 4; ++jq) lv[jq] = lds_read<f32x4>(st + QT_B + 4 * (32 * mb + 8 * jq + 4 * g));
@@ -1226,7 +1177,7 @@ attn_colsum_d128_kernel(AttnParams p) {
         else
           pe = fast_exp2(fmaf(x, c, -l2));
         bool valid = true;
-        if (per_elem) {
+        if constexpr (decltype(masked)::value) {
           valid = o < rows_left;
           bool ok = valid;
           if constexpr (MASK) {

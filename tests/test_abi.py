@@ -141,6 +141,17 @@ def test_topk_validation(lib):
     assert lib.dgg_topk_indices(None, 0, 100, 10, None, None) == OK
 
 
+def test_ref_multiplier_validation(lib):
+    y = ctypes.c_float(0.0)
+    assert lib.dgg_ref_multiplier(_lib.DGG_F32, 11.0, ctypes.byref(y)) == E_DTYPE
+    assert lib.dgg_ref_multiplier(_lib.DGG_F16, 11.0, None) == E_NULL
+    # a divisor with an exact reciprocal: the multiplier is found and is that reciprocal
+    assert lib.dgg_ref_multiplier(_lib.DGG_BF16, 4.0, ctypes.byref(y)) == 1
+    assert y.value == 0.25
+    # not finite: no multiplier (the kernels then keep the division sequence)
+    assert lib.dgg_ref_multiplier(_lib.DGG_F16, float("inf"), ctypes.byref(y)) == 0
+
+
 def test_python_wrappers_reject_cpu_tensors():
     import torch
 

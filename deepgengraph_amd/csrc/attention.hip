@@ -1,20 +1,24 @@
-// Fused online-softmax attention for gfx950 (CDNA4): prefill forward (causal / sliding window / tanh
-// soft-cap / GQA) and the H2O probability column-sum pass.
+// Fused online-softmax attention for gfx950 (CDNA4): prefill forward (causal / sliding window / tanh soft-cap /
+// GQA), the column-score passes of the selection cases (H2O, RoCo, SnapKV, Corm, KeyFormer) and KeyFormer's
+// perturbed row log-sum-exp.
 //
-// Tiling (forward). A workgroup of 4 wave64s owns BM = 128 query rows of one (batch, head); wave w owns
-// rows 32w..32w+31. K/V are streamed in tiles of BN keys through double-buffered LDS: K row-major
-// [key][d] and V transposed [d][key]. Both products run on v_mfma_f32_32x32x16_{bf16,f16}:
-//   S^T (BN x 32)  = K (BN x D) . Q^T (D x 32)     A = K from LDS, B = Q held in VGPRs for the whole loop
-//   O^T (D x 32)  += V^T (D x BN) . P^T (BN x 32)  A = V^T from LDS, B = P straight from the S^T accumulator
-// Computing S transposed puts one query per lane (column n = lane % 32) with its keys spread over the
-// lane's accumulator registers and the partner lane (lane ^ 32). Row max / row sum are therefore in-lane
-// plus one cross-half exchange, and the fp32 accumulator, rounded to 16 bits, is already laid out as the
-// B operand of the P.V product (both operands use the same key order, so no LDS round trip for P).
-// Softmax runs in the exp2 domain with a lazily-updated row maximum: O and l are rescaled only when a
-// row's maximum grows by more than 2^8, so P stays <= 256 and the 64-register O rescale is rare.
-// Causal / window tiles are skipped per workgroup; only tiles that straddle the mask boundary (or the
-// ragged end of K) evaluate the per-element mask. Workgroups are ordered longest-first and grouped by
-// head inside each XCD (blockIdx round-robins over the 8 XCDs) so the K/V of a head stay in one L2.
+// Products. Both run on v_mfma_f32_32x32x16_{bf16,f16} with the scores computed transposed:
+//   S^T (BN x 32)  = K (BN x D) . Q^T (D x 32)     A = K fragments from LDS, B = Q held in registers
+//   O^T (D x 32)  += V^T (D x BN) . P^T (BN x 32)  A = V^T by transposing LDS reads (ds_read_b64_tr_b16) of the
+//                                                   row-major V tile, B = P straight from the S^T accumulator
+// One query per lane (column n = lane % 32): the row max and row sum are in-lane plus one cross-half exchange
+// (v_permlane32_swap), and the accumulator, rounded to 16 bits, is already the B operand of P.V.
+// Softmax runs in the exp2 domain with a lazily-updated row maximum: O and l are rescaled only when a row's
+// maximum grows by more than 2^8.
+//
+// Kernels. attn_fwd_dma_kernel (head_dim 128: 8 waves x 32 rows, 128-key tiles; head_dim 256: 4 waves, 64-key
+// tiles) copies K/V tiles global -> LDS with direct loads (global_load_lds_dwordx4) into a swizzled ring;
+// attn_fwd_kernel (head_dim 64) stages them through registers. Tiles a wave cannot see are skipped, and within
+// masked tiles dead 32-key blocks skip their MFMAs. attn_colsum_d128_kernel / attn_colsum_kernel recompute
+// P = exp2(s - lse) with one key per lane and sum (or test) it over the queries; attn_kf_rowlse_kernel is the
+// row pass of KeyFormer's perturbed softmax. Reference rounding (DGG_ATTN_REF_ROUNDING) rounds the scores as
+// the reference does, by the exact division sequence (mode 1) or a host-verified multiplier (mode 2).
+// Workgroups are ordered longest-first and grouped by head inside each XCD so the K/V of a head stay in one L2.
 #include <algorithm>
 #include <cstring>
 #include <mutex>

@@ -117,18 +117,21 @@ def _colsum_check(got, ref, what):
     assert_close(got, ref, 1e-6, 1e-3, what)
 
 
-@pytest.mark.parametrize("S,H,D,sinks", [(256, 2, 128, 4), (1000, 4, 128, 16), (300, 2, 64, 3)])
-def test_h2o_matches_oracle(gpu, S, H, D, sinks):
+@pytest.mark.parametrize("S,H,D,sinks,dtype", [
+    (256, 2, 128, 4, torch.float16), (1000, 4, 128, 16, torch.float16), (300, 2, 64, 3, torch.float16),
+    (512, 2, 128, 4, torch.bfloat16),   # bf16 scores rounded through the host-verified bf16 multiplier
+])
+def test_h2o_matches_oracle(gpu, S, H, D, sinks, dtype):
     g = torch.Generator().manual_seed(S + H)
     q = torch.randn(1, S, H, D, generator=g)
     k = torch.randn(1, S, H, D, generator=g)
     v = torch.randn(1, S, H, D, generator=g)
     k[:, torch.randperm(S, generator=g)[:sinks]] *= 4.0
-    q, k, v = q.half(), k.half(), v.half()
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
     ref_out, ref_cs, ref_lse = oa.h2o(q, k, v)
     out, cs = A.h2o_attention(q.to(gpu), k.to(gpu), v.to(gpu))
-    what = f"h2o S{S} H{H} D{D}"
-    assert_close(out.cpu().float(), ref_out.float(), 1e-2, 5e-3, what + " out")
+    what = f"h2o S{S} H{H} D{D} {dtype}"
+    assert_close(out.cpu().float(), ref_out.float(), *TOL[dtype], what + " out")
     _colsum_check(cs.cpu(), ref_cs, what + " colsum")
     assert_close(cs.sum(-1).cpu(), torch.full((1, H), float(S)), 0, 1e-4, what + " sum of colsums = q_len")
     kk = min(64, S // 4)

@@ -6,6 +6,9 @@
   deepgengraph_amd.compile    compile(model, input_names, inputs, output_names, system='mi355x') -> f(*inputs)
   deepgengraph_amd.llama      the Llama-2 attention block (config 2) and decode pre-step (config 5) on these ops
   deepgengraph_amd.configs    the five benchmark configurations as seeded input builders
+  deepgengraph_amd.cases      the reference's attention case modules (Attn, Gemma2, H2O, RoCo, SnapKV, Corm, KeyFormer)
+  deepgengraph_amd.run_kernel the per-case harness (run_kernel.py's CLI and perf line)
+  deepgengraph_amd.run_e2e    the end-to-end harness: random-weight Llama-2-7B with each case's KV-cache selection
 
 All GPU work runs in libdgg_hip.so (C ABI: include/dgg.h), loaded with ctypes; there is no CPU fallback.
 """

@@ -19,6 +19,17 @@ def _check_bshd(name: str, t: torch.Tensor):
         raise RuntimeError(f"{name}: head dimension must be contiguous (stride {t.stride(-1)})")
 
 
+def _check_qk(name: str, q: torch.Tensor, k: torch.Tensor):
+    """q [B, Sq, Hq, D] and k [B, Sk, Hkv, D] as the column kernels read them: k's batch, head dim and dtype are
+    taken from q."""
+    _check_bshd("q", q)
+    _check_bshd("k", k)
+    if k.shape[0] != q.shape[0] or k.shape[3] != q.shape[3]:
+        raise RuntimeError(f"{name}: incompatible shapes q {tuple(q.shape)} k {tuple(k.shape)}")
+    if k.dtype != q.dtype:
+        raise RuntimeError(f"{name}: q and k dtypes differ")
+
+
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool = True, softcap: float = 0.0,
               window: int = 0, scale: float | None = None, return_lse: bool = False, ref_rounding: bool = False,
               out: torch.Tensor | None = None, lse_base2: bool = False):
@@ -63,8 +74,7 @@ def attention_colsum(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor, *, cau
     """Column sums of the softmax probabilities over the query axis, per query head: [B, Hq, Sk] fp32, recomputed
     from q, k and the lse written by attention(..., return_lse=True) with the same options (lse_base2 included)."""
     dev = _lib.require_gpu(q, k, lse)
-    _check_bshd("q", q)
-    _check_bshd("k", k)
+    _check_qk("attention_colsum", q, k)
     B, Sq, Hq, D = q.shape
     Sk, Hkv = k.shape[1], k.shape[2]
     if lse.shape != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
@@ -100,8 +110,7 @@ def attention_colscore(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor, *, e
     epilogue COL_SUM -> sum_i p; COL_SUM_SQ -> (sum_i p, sum_i p^2) (roco.py:43-47); COL_ANY_GE -> bool
     any_i p[i, j] >= thr[i, j] with thr fp32 [Sq, Sk] (corm.py:35-37)."""
     dev = _lib.require_gpu(q, k, lse, thr)
-    _check_bshd("q", q)
-    _check_bshd("k", k)
+    _check_qk("attention_colscore", q, k)
     B, Sq, Hq, D = q.shape
     Sk, Hkv = k.shape[1], k.shape[2]
     if lse.shape != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
@@ -184,8 +193,9 @@ def keyformer_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exp_r
     kf_score [B, H, Sk] fp32, the column sums over the queries of softmax((scores + gumbels) / tau) with
     gumbels = -log(exp_rand) (kf.py:36-40); exp_rand fp32 [B, H, Sq, Sk] (unit key stride). MHA, as kf.py:16
     asserts. Three launches: the forward, the perturbed row lse, the column pass."""
-    _require_mha("keyformer_attention", q, k)
     dev = _lib.require_gpu(q, k, v, exp_rand)
+    _check_qk("keyformer_attention", q, k)
+    _require_mha("keyformer_attention", q, k)
     B, Sq, H, D = q.shape
     Sk = k.shape[1]
     if (exp_rand.dtype != torch.float32 or exp_rand.dim() != 4 or tuple(exp_rand.shape) != (B, H, Sq, Sk)
@@ -289,6 +299,8 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
         raise RuntimeError("decode_attention: invalid sizes")
     if workspace is None:
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
+    elif not workspace.is_contiguous():
+        raise RuntimeError("decode_attention: workspace must be contiguous")
     ws_bytes = workspace.numel() * workspace.element_size()
     lse = torch.empty(B, Hq, dtype=torch.float32, device=q.device) if return_lse else None
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)

@@ -54,8 +54,8 @@ def fused_add_rms_norm(input: torch.Tensor, residual: torch.Tensor, weight: torc
     if input.shape != residual.shape:
         raise RuntimeError("fused_add_rms_norm: input and residual shapes differ")
     hidden = input.shape[-1]
-    if weight.numel() != hidden:
-        raise RuntimeError(f"fused_add_rms_norm: weight must have {hidden} elements")
+    if weight.numel() != hidden or (weight.dim() > 0 and weight.stride(-1) != 1 and hidden > 1):
+        raise RuntimeError(f"fused_add_rms_norm: weight must be a contiguous vector of {hidden} elements")
     rows, in_rs = _rows(input, "fused_add_rms_norm input")
     _, res_rs = _rows(residual, "fused_add_rms_norm residual")
     _lib.call("dgg_fused_add_rms_norm", _lib.ptr(input), _lib.ptr(residual), _lib.ptr(weight), rows, hidden, in_rs,
@@ -90,6 +90,8 @@ def rotary_embedding_online(positions: torch.Tensor, query: torch.Tensor, key: t
         raise RuntimeError(f"rotary_embedding_online: positions must be int32 (got {positions.dtype})")
     if key is not None and key.dtype != query.dtype:
         raise RuntimeError("rotary_embedding_online: query and key dtypes differ")
+    if head_size <= 0:
+        raise RuntimeError(f"rotary_embedding_online: head_size {head_size} must be positive")
     width = query.shape[-1]
     if width % head_size:
         raise RuntimeError(f"rotary_embedding_online: query width {width} is not a multiple of head_size {head_size}")

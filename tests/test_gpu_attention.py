@@ -174,6 +174,25 @@ def test_colsum_variants(gpu, D, Sq, Sk, causal, window, softcap, dtype, base2):
     assert_close(cs, ref, 1e-3, 1e-2, what + " (kernel keeps fp32 scores, reference fp32)")
 
 
+def test_column_wrappers_reject_mismatched_k(gpu):
+    # the column kernels take k's batch, head dim and dtype from q: a k that differs is refused on the host
+    q = torch.zeros(1, 64, 2, 128, dtype=torch.bfloat16, device=gpu)
+    lse = torch.zeros(1, 2, 64, dtype=torch.float32, device=gpu)
+    bad = {"head dim": torch.zeros(1, 64, 2, 64, dtype=torch.bfloat16, device=gpu),
+           "batch": torch.zeros(2, 64, 2, 128, dtype=torch.bfloat16, device=gpu),
+           "dtype": torch.zeros(1, 64, 2, 128, dtype=torch.float16, device=gpu)}
+    for what, k in bad.items():
+        with pytest.raises(RuntimeError, match="incompatible shapes|dtypes differ"):
+            A.attention_colsum(q, k, lse)
+        with pytest.raises(RuntimeError, match="incompatible shapes|dtypes differ"):
+            A.attention_colscore(q, k, lse, epilogue=0)
+    ws = torch.zeros(1 << 20, dtype=torch.uint8, device=gpu)[::2]
+    with pytest.raises(RuntimeError, match="workspace must be contiguous"):
+        A.decode_attention(torch.zeros(1, 2, 128, dtype=torch.bfloat16, device=gpu),
+                           torch.zeros(1, 2, 64, 128, dtype=torch.bfloat16, device=gpu),
+                           torch.zeros(1, 2, 64, 128, dtype=torch.bfloat16, device=gpu), workspace=ws)
+
+
 def test_topk_kernel_golden_and_ties(gpu):
     g = load_golden("topk_ties")
     x = torch.from_numpy(g["x"]).to(gpu)

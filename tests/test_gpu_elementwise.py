@@ -155,3 +155,7 @@ def test_wrapper_errors(gpu):
     with pytest.raises(RuntimeError, match="head_dim"):
         ops.rotary_embedding_online(torch.zeros(4, dtype=torch.int32, device=gpu), torch.zeros(4, 100, device=gpu,
                                     dtype=torch.float16), None, 100, 1e4)
+    with pytest.raises(RuntimeError, match="contiguous vector"):
+        ops.fused_add_rms_norm(h, h.clone(), torch.ones(128, dtype=torch.float16, device=gpu)[::2], 1e-6)
+    with pytest.raises(RuntimeError, match="must be positive"):
+        ops.rotary_embedding_online(torch.zeros(4, dtype=torch.int32, device=gpu), h, None, 0, 1e4)

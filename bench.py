@@ -31,18 +31,20 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16/fp16 MFMA
 PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
 
 
-def _events_time(fn, iters: int, warmup: int) -> list[float]:
-    """Runs fn warmup + iters times; returns per-call GPU durations (ms) from event pairs on the current stream."""
+def _events_time(fn, iters: int, warmup: int) -> float:
+    """Runs fn warmup + iters times; returns the mean GPU duration of one call (ms) from a HIP event pair on the
+    current stream around each call. The pairs bracket the kernels alone, so the figure holds also for kernels
+    shorter than the host's launch cost; the markers' own cost (~7 us per pair) falls between the pairs."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
-    for s, e in evs:
-        s.record()
+    for start, end in evs:
+        start.record()
         fn()
-        e.record()
+        end.record()
     torch.cuda.synchronize()
-    return [s.elapsed_time(e) for s, e in evs]
+    return statistics.mean(start.elapsed_time(end) for start, end in evs)
 
 
 def bench_prefill(args, dev):
@@ -55,18 +57,20 @@ def bench_prefill(args, dev):
     fn = lambda: A.attention(q, k, v, causal=True, out=out)  # noqa: E731
     for _ in range(args.warmup):
         fn()
-    # Timed region: K back-to-back steps between two synchronisations; a HIP event pair around each launch on the
-    # launch stream gives the kernel's own durations inside the same region (the roofline figure).
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    # Timed region: K back-to-back steps between two synchronisations. One HIP event pair on the launch stream
+    # brackets the same K launches; nothing else runs on the GPU in between, so its elapsed time / K is the
+    # kernel's average launch duration (the roofline figure; it also counts whatever gap the GPU leaves between
+    # two launches). An event pair around every launch would add ~7 us of its own to each step.
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for s, e in evs:
-        s.record()
+    start.record()
+    for _ in range(args.steps):
         fn()
-        e.record()
+    end.record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    kern_ms = statistics.mean([s.elapsed_time(e) for s, e in evs])
+    kern_ms = start.elapsed_time(end) / args.steps
     flops = cfg.reference_flops()
     return dict(cfg=cfg, wall_ms=wall_ms, kern_ms=kern_ms, flops=flops, exact_flops=cfg.flops(),
                 tflops_wall=flops / (wall_ms * 1e-3) / 1e12, tflops_kern=flops / (kern_ms * 1e-3) / 1e12)
@@ -81,7 +85,7 @@ def bench_decode(args, dev):
     ws = torch.empty(A.decode_workspace_bytes(cfg.B, cfg.Hq, cfg.D, cfg.splits), dtype=torch.uint8, device=dev)
     out = torch.empty_like(q)
     fn = lambda: A.decode_attention(q, kc, vc, splits=cfg.splits, out=out, workspace=ws)  # noqa: E731
-    ms = statistics.mean(_events_time(fn, max(5, args.steps // 2), 2))
+    ms = _events_time(fn, max(5, args.steps // 2), 2)
     nbytes = cfg.bytes()
     del kc, vc
     torch.cuda.empty_cache()
@@ -100,30 +104,30 @@ def bench_prestep(args, dev):
     act = torch.empty(cfg.B, cfg.intermediate, dtype=cfg.dtype, device=dev)
     e = pre["x"].element_size()
     res = {}
-    ms = statistics.mean(_events_time(lambda: ops.rms_norm(normed, pre["x"], pre["w_norm"], C.LLAMA_EPS), 20, 3))
+    ms = _events_time(lambda: ops.rms_norm(normed, pre["x"], pre["w_norm"], C.LLAMA_EPS), 20, 3)
     nb = e * (2 * pre["x"].numel() + pre["w_norm"].numel())
     res["rms_norm_64x4096_f16"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1))
-    ms = statistics.mean(_events_time(lambda: ops.silu_and_mul(act, pre["gate_up"]), 20, 3))
+    ms = _events_time(lambda: ops.silu_and_mul(act, pre["gate_up"]), 20, 3)
     nb = e * (pre["gate_up"].numel() + act.numel())
     res["silu_and_mul_64x11008_f16"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1))
     # config-2 sized elementwise kernels (bandwidth-meaningful sizes)
     x = torch.randn(4096, 4096, device=dev).bfloat16()
     w = torch.ones(4096, device=dev).bfloat16()
     y = torch.empty_like(x)
-    ms = statistics.mean(_events_time(lambda: ops.rms_norm(y, x, w, 1e-6), 20, 3))
+    ms = _events_time(lambda: ops.rms_norm(y, x, w, 1e-6), 20, 3)
     nb = 2 * (2 * x.numel() + w.numel())
     res["rms_norm_4096x4096_bf16"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1),
                                           frac=round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4))
     qkv = torch.randn(4096, 3 * 4096, device=dev).bfloat16()
     pos = torch.arange(4096, dtype=torch.int32, device=dev)
-    ms = statistics.mean(_events_time(
-        lambda: ops.rotary_embedding_online(pos, qkv[:, :4096], qkv[:, 4096:8192], 128, 1e4), 20, 3))
+    ms = _events_time(
+        lambda: ops.rotary_embedding_online(pos, qkv[:, :4096], qkv[:, 4096:8192], 128, 1e4), 20, 3)
     nb = 2 * 2 * (2 * 4096 * 4096) + 4 * 4096
     res["rotary_4096tok_32+32heads_bf16"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1),
                                                  frac=round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4))
     gu = torch.randn(4096, 2 * 11008, device=dev).bfloat16()
     a = torch.empty(4096, 11008, device=dev, dtype=torch.bfloat16)
-    ms = statistics.mean(_events_time(lambda: ops.silu_and_mul(a, gu), 20, 3))
+    ms = _events_time(lambda: ops.silu_and_mul(a, gu), 20, 3)
     nb = 2 * (gu.numel() + a.numel())
     res["silu_and_mul_4096x11008_bf16"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1),
                                                frac=round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4))
@@ -137,14 +141,14 @@ def bench_variants(args, dev):
     res = {}
     cfg = C.CFG3
     q, k, v, _ = C.attn_inputs(cfg, device=dev)
-    ms = statistics.mean(_events_time(
-        lambda: A.attention(q, k, v, causal=True, softcap=cfg.softcap, window=cfg.window), 10, 3))
+    ms = _events_time(
+        lambda: A.attention(q, k, v, causal=True, softcap=cfg.softcap, window=cfg.window), 10, 3)
     res["cfg3_gemma2"] = dict(ms=round(ms, 4), tflops=round(cfg.flops() / (ms * 1e-3) / 1e12, 1),
                               frac=round(cfg.flops() / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))
     del q, k, v
     cfg = C.CFG4
     q, k, v, _ = C.attn_inputs(cfg, device=dev)
-    ms = statistics.mean(_events_time(lambda: A.topk_indices(A.h2o_attention(q, k, v)[1], cfg.topk), 5, 1))
+    ms = _events_time(lambda: A.topk_indices(A.h2o_attention(q, k, v)[1], cfg.topk), 5, 1)
     res["cfg4_h2o_fwd_colsum_topk"] = dict(ms=round(ms, 4),
                                            tflops=round(cfg.reference_flops() / (ms * 1e-3) / 1e12, 1),
                                            frac=round(cfg.reference_flops() / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))
@@ -153,18 +157,18 @@ def bench_variants(args, dev):
     for name, fn in (("cfg4_roco", lambda: A.roco_attention(q, k, v)),
                      ("cfg4_snapkv", lambda: A.snapkv_attention(q, k, v)),
                      ("cfg4_corm", lambda: A.corm_attention(q, k, v, thr))):
-        ms = statistics.mean(_events_time(fn, 5, 1))
+        ms = _events_time(fn, 5, 1)
         res[name] = dict(ms=round(ms, 4), tflops=round(cfg.reference_flops() / (ms * 1e-3) / 1e12, 1))
     # KeyFormer (kf.py): exp_rand [1, 32, 4096, 4096] fp32 (1 + |N(0,1)|, kf.py:48); its causal half is read twice
     # (row lse pass, column pass)
     er = 1 + torch.randn(cfg.B, cfg.Hq, cfg.Sq, cfg.Sk, device=dev).abs()
-    ms = statistics.mean(_events_time(lambda: A.keyformer_attention(q, k, v, er), 5, 1))
+    ms = _events_time(lambda: A.keyformer_attention(q, k, v, er), 5, 1)
     er_bytes = 2 * cfg.B * cfg.Hq * (cfg.Sq * (cfg.Sq + 1) // 2) * 4
     res["cfg4_keyformer"] = dict(ms=round(ms, 4), tflops=round(cfg.reference_flops() / (ms * 1e-3) / 1e12, 1),
                                  exp_rand_gbps=round(er_bytes / (ms * 1e-3) / 1e9, 1))
     del er
     idx = A.topk_indices(A.h2o_attention(q, k, v)[1], cfg.topk)
-    ms = statistics.mean(_events_time(lambda: A.kv_gather(k, v, idx), 20, 2))
+    ms = _events_time(lambda: A.kv_gather(k, v, idx), 20, 2)
     nb = 2 * 2 * idx.numel() * cfg.D * k.element_size()  # K and V rows read once and written once
     res["cfg4_kv_gather_top256"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1))
     return res
@@ -177,7 +181,7 @@ def bench_block(args, dev):
     inp = C.llama_block_inputs(device=dev)
     blk = LlamaAttentionBlock(inp["w_norm"], inp["w_qkv"], inp["w_o"], heads=32, kv_heads=32, eps=C.LLAMA_EPS,
                               rope_theta=C.LLAMA_THETA)
-    ms = statistics.mean(_events_time(lambda: blk(inp["x"]), 10, 2))
+    ms = _events_time(lambda: blk(inp["x"]), 10, 2)
     return dict(ms=round(ms, 4))
 
 
@@ -187,7 +191,7 @@ def bench_copycal(args, dev):
     n = 256 * 1024 * 1024
     src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
-    ms = statistics.mean(_events_time(lambda: dst.copy_(src), 5, 1))
+    ms = _events_time(lambda: dst.copy_(src), 5, 1)
     return dict(bytes_read=n, bytes_written=n, ms=round(ms, 4), gbps=round(2 * n / (ms * 1e-3) / 1e9, 1))
 
 

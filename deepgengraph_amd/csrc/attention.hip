@@ -1234,7 +1234,13 @@ void launch_colsum(const AttnParams& p, hipStream_t st) {
 }
 
 // head_dim 128 configuration (measured on MI355X, config 2): 8 waves x 32 rows, 128-key tiles, 2-stage ring.
-constexpr int kD128NQB = 1, kD128NW = 8, kD128BN = 128, kD128NS = 2;
+#ifndef DGG_D128_NW
+#define DGG_D128_NW 8
+#endif
+#ifndef DGG_D128_BN
+#define DGG_D128_BN 128
+#endif
+constexpr int kD128NQB = 1, kD128NW = DGG_D128_NW, kD128BN = DGG_D128_BN, kD128NS = 2;
 constexpr int kD128BM = 32 * kD128NQB * kD128NW;  // query rows per workgroup (head_dim 128)
 
 template <typename T, bool MASK, bool SOFTCAP, int REFROUND>

@@ -179,7 +179,8 @@ __global__ void __launch_bounds__(256) silu_and_mul_scalar_kernel(typename T::sc
 // ---------------------------------------------------------------------------------------------
 // Online rotary (csrc/pos_encoding.cu:64-113). One workgroup per token: the D/2 (cos, sin) pairs are
 // computed once into LDS with accurate powf / sincosf (angles reach thousands of radians), then every
-// (head, 8-pair group) of q and k is rotated with 16-byte loads. VEC=false: scalar element path.
+// (head, 8-pair group) of q and k is rotated with 16-byte loads, the first two per thread issued before the
+// angles are computed. VEC=false: scalar element path.
 // ---------------------------------------------------------------------------------------------
 template <typename T, bool VEC>
 __global__ void __launch_bounds__(256) rotary_online_kernel(const int32_t* __restrict__ pos,
@@ -188,47 +189,82 @@ __global__ void __launch_bounds__(256) rotary_online_kernel(const int32_t* __res
                                                              int hk, int D, int64_t q_rs, int64_t k_rs,
                                                              float theta) {
   __shared__ float cs[256], sn[256];
+  typedef typename T::scalar S;
   const int half = D / 2;
   const int64_t tok = blockIdx.x;
   const float p = (float)pos[tok];
-  for (int i = threadIdx.x; i < half; i += blockDim.x) {
-    const float ang = p / powf(theta, (float)(2 * i) / (float)D);
-    float s, c;
-    sincosf(ang, &s, &c);
-    cs[i] = c;
-    sn[i] = s;
-  }
-  __syncthreads();
+  auto angles = [&]() {
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+      const float ang = p / powf(theta, (float)(2 * i) / (float)D);
+      float s, c;
+      sincosf(ang, &s, &c);
+      cs[i] = c;
+      sn[i] = s;
+    }
+  };
   if constexpr (VEC) {
     typedef typename VecOf<T>::type V;
     constexpr int EPV = VecOf<T>::EPV;
+    // Items (head, 8-pair group) of this thread whose loads are issued before the angles are computed, so that
+    // the memory latency and the powf / sincosf latency overlap (two per thread at 32 + 32 heads of 128).
+    constexpr int PF = 2;
     const int gph = half / EPV;  // pair groups per head
     const int items = (hq + hk) * gph;
-    for (int it = threadIdx.x; it < items; it += blockDim.x) {
+    auto item_base = [&](int it, int& i0) -> S* {
       const int h = it / gph, gi = it - h * gph;
-      typename T::scalar* base = h < hq ? q + tok * q_rs + (int64_t)h * D : k + tok * k_rs + (int64_t)(h - hq) * D;
-      const int i0 = gi * EPV;
-      V x = ld16<V>(base + i0), y = ld16<V>(base + half + i0);
+      i0 = gi * EPV;
+      return h < hq ? q + tok * q_rs + (int64_t)h * D : k + tok * k_rs + (int64_t)(h - hq) * D;
+    };
+    auto rotate = [&](S* base, int i0, const V& x, const V& y) {
       V xo, yo;
 #pragma unroll
       for (int e = 0; e < EPV; ++e) {
         const float c = cs[i0 + e], s = sn[i0 + e];
         const float xf = to_f(x[e]), yf = to_f(y[e]);
-        xo[e] = to_s<typename T::scalar>(xf * c - yf * s);
-        yo[e] = to_s<typename T::scalar>(yf * c + xf * s);
+        xo[e] = to_s<S>(xf * c - yf * s);
+        yo[e] = to_s<S>(yf * c + xf * s);
       }
       st16<V>(base + i0, xo);
       st16<V>(base + half + i0, yo);
+    };
+    V px[PF], py[PF];
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int it = threadIdx.x + j * blockDim.x;
+      if (it < items) {
+        int i0;
+        const S* base = item_base(it, i0);
+        px[j] = ld16<V>(base + i0);
+        py[j] = ld16<V>(base + half + i0);
+      }
+    }
+    angles();
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int it = threadIdx.x + j * blockDim.x;
+      if (it < items) {
+        int i0;
+        S* base = item_base(it, i0);
+        rotate(base, i0, px[j], py[j]);
+      }
+    }
+    for (int it = threadIdx.x + PF * blockDim.x; it < items; it += blockDim.x) {
+      int i0;
+      S* base = item_base(it, i0);
+      rotate(base, i0, ld16<V>(base + i0), ld16<V>(base + half + i0));
     }
   } else {
+    angles();
+    __syncthreads();
     const int items = (hq + hk) * half;
     for (int it = threadIdx.x; it < items; it += blockDim.x) {
       const int h = it / half, i = it - h * half;
-      typename T::scalar* base = h < hq ? q + tok * q_rs + (int64_t)h * D : k + tok * k_rs + (int64_t)(h - hq) * D;
+      S* base = h < hq ? q + tok * q_rs + (int64_t)h * D : k + tok * k_rs + (int64_t)(h - hq) * D;
       const float xf = to_f(base[i]), yf = to_f(base[half + i]);
       const float c = cs[i], s = sn[i];
-      base[i] = to_s<typename T::scalar>(xf * c - yf * s);
-      base[half + i] = to_s<typename T::scalar>(yf * c + xf * s);
+      base[i] = to_s<S>(xf * c - yf * s);
+      base[half + i] = to_s<S>(yf * c + xf * s);
     }
   }
 }

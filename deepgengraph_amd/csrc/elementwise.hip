@@ -47,7 +47,8 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// RMSNorm (csrc/norm.cu:34-56). Vector path: the row is read once into registers (NV chunks per thread).
+// RMSNorm (csrc/norm.cu:34-56). Vector path: the row is read once into registers (NV chunks per thread),
+// together with the matching weight chunks.
 // RESID: fused residual add (csrc/norm.cu:59-83): v = in + res; res = T(v); variance from the unrounded v;
 // output from the rounded residual.
 // ---------------------------------------------------------------------------------------------
@@ -65,12 +66,14 @@ __global__ void __launch_bounds__(1024) rms_norm_vec_kernel(typename T::scalar* 
   const int nvec = hidden / EPV;
   const typename T::scalar* x = in + row * in_rs;
   float vals[NV][EPV];
+  V wv[NV];  // the weight slice, loaded with the row so that its latency is not paid after the reduction
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = threadIdx.x + i * blockDim.x;
     if (c < nvec) {
       V a = ld16<V>(x + (int64_t)c * EPV);
+      wv[i] = ld16<V>(w + (int64_t)c * EPV);
       if constexpr (RESID) {
         typename T::scalar* r = res + row * res_rs + (int64_t)c * EPV;
         V b = ld16<V>(r);
@@ -100,10 +103,9 @@ __global__ void __launch_bounds__(1024) rms_norm_vec_kernel(typename T::scalar* 
   for (int i = 0; i < NV; ++i) {
     const int c = threadIdx.x + i * blockDim.x;
     if (c < nvec) {
-      V wv = ld16<V>(w + (int64_t)c * EPV);
       V o;
 #pragma unroll
-      for (int e = 0; e < EPV; ++e) o[e] = to_s<typename T::scalar>(round_t<T>(vals[i][e] * s) * to_f(wv[e]));
+      for (int e = 0; e < EPV; ++e) o[e] = to_s<typename T::scalar>(round_t<T>(vals[i][e] * s) * to_f(wv[i][e]));
       st16<V>(y + (int64_t)c * EPV, o);
     }
   }

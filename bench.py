@@ -31,20 +31,44 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16/fp16 MFMA
 PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
 
 
+_COVER = {}  # device -> buffer of the fill that _events_time queues its timed calls behind
+
+
 def _events_time(fn, iters: int, warmup: int) -> float:
-    """Runs fn warmup + iters times; returns the mean GPU duration of one call (ms) from a HIP event pair on the
-    current stream around each call. The pairs bracket the kernels alone, so the figure holds also for kernels
-    shorter than the host's launch cost; the markers' own cost (~7 us per pair) falls between the pairs."""
+    """Runs fn warmup + iters times; returns the mean GPU time of one call (ms) over iters back-to-back calls,
+    from one HIP event pair on the current stream around them.
+
+    The timed calls are queued behind a device fill (512 MiB, repeated) that keeps the GPU busy while the host
+    enqueues them, so the host's launch cost (~12 us per call through the Python wrappers) cannot starve the GPU
+    between short kernels. A run counts when the start event was still pending after the last call had been
+    enqueued, or when a call takes the GPU more than twice as long as the host takes to enqueue it (then the host
+    stays ahead); otherwise the cover is made 4x longer and the run repeated. An event pair around each call would
+    instead count ~3 us of marker handling inside every bracket (12.6 us kernels read 16 us)."""
+    dev = torch.cuda.current_device()
+    if dev not in _COVER:
+        _COVER[dev] = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    cover = _COVER[dev]
     for _ in range(warmup):
         fn()
-    torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
-    for start, end in evs:
+    reps = 2
+    for _ in range(5):
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(reps):
+            cover.fill_(0)
         start.record()
-        fn()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        host_s = time.perf_counter() - t0
+        covered = not start.query()
         end.record()
-    torch.cuda.synchronize()
-    return statistics.mean(start.elapsed_time(end) for start, end in evs)
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / iters
+        if covered or ms * 1e-3 > 2.0 * host_s / iters:
+            break
+        reps *= 4
+    return ms
 
 
 def bench_prefill(args, dev):

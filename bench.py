@@ -10,9 +10,11 @@ sections report configs 3 and 4, the config-2 block and the elementwise kernels.
 HIP events recorded on the stream the kernels are launched on (torch's current stream). The CPU baseline is
 the oracle (reference formula in PyTorch eager on the host cores) on a bounded sample of config 2.
 
-Warm-up: under a sustained load the part raises its shader clock over the first ~400 launches of this kernel
-(averages per 50 launches measured on MI355X: 159, 142, 137, ..., then a steady ~128 us from launch ~400 on), so
-the default warm-up of 500 steps (~70 ms) puts the timed steps at the steady-state clock.
+Clock: under a sustained load the part raises its shader clock over the first few hundred launches of this kernel,
+so a short warm-up times the kernel at a lower clock than a long one. The line records the shader clock measured
+right before and right after the timed region (`clock_mhz`, a one-lane probe reading the cycle counter against the
+100 MHz real-time counter), and, apart from `value`, a `steady` figure: the same kernel timed again after the
+launches so far are topped up to STEADY_WARMUP, with its own clock reading.
 """
 from __future__ import annotations
 
@@ -27,6 +29,8 @@ import time
 import torch
 
 METRIC = "attention TFLOP/s (% bf16 MFMA peak) + decode HBM GB/s, Llama-2-7B shapes"
+STEADY_WARMUP = 600  # launches before the `steady` figure is timed
+STEADY_STEPS = 200
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16/fp16 MFMA
 PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
 
@@ -71,6 +75,18 @@ def _events_time(fn, iters: int, warmup: int) -> float:
     return ms
 
 
+def _clock_probe(dev, buf, slot):
+    """Enqueues the shader-clock probe (20 us spin) on the current stream; its result lands in buf[slot]."""
+    from deepgengraph_amd import _lib
+
+    _lib.call("dgg_clock_probe", _lib.ptr(buf[slot]), 2000, _lib.stream_handle(dev))
+
+
+def _clock_mhz(buf, slot):
+    cyc, ticks = buf[slot].tolist()
+    return round(cyc / ticks * 100.0, 1) if ticks > 0 else None
+
+
 def bench_prefill(args, dev):
     from deepgengraph_amd import attention as A
     from deepgengraph_amd import configs as C
@@ -79,8 +95,10 @@ def bench_prefill(args, dev):
     q, k, v, _ = C.attn_inputs(cfg, device=dev)
     out = torch.empty_like(q)
     fn = lambda: A.attention(q, k, v, causal=True, out=out)  # noqa: E731
+    clk = torch.zeros(4, 2, dtype=torch.int64, device=dev)
     for _ in range(args.warmup):
         fn()
+    _clock_probe(dev, clk, 0)
     # Timed region: K back-to-back steps between two synchronisations. One HIP event pair on the launch stream
     # brackets the same K launches; nothing else runs on the GPU in between, so its elapsed time / K is the
     # kernel's average launch duration (the roofline figure; it also counts whatever gap the GPU leaves between
@@ -95,9 +113,27 @@ def bench_prefill(args, dev):
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     kern_ms = start.elapsed_time(end) / args.steps
+    _clock_probe(dev, clk, 1)
+    # steady figure (not `value`): top the launches up to STEADY_WARMUP, then time STEADY_STEPS more
+    for _ in range(max(0, STEADY_WARMUP - args.warmup - args.steps)):
+        fn()
+    _clock_probe(dev, clk, 2)
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record()
+    for _ in range(STEADY_STEPS):
+        fn()
+    s1.record()
+    _clock_probe(dev, clk, 3)
+    torch.cuda.synchronize()
+    steady_ms = s0.elapsed_time(s1) / STEADY_STEPS
     flops = cfg.reference_flops()
+    steady = dict(warmup_launches=max(STEADY_WARMUP, args.warmup + args.steps), steps=STEADY_STEPS,
+                  kernel_ms=round(steady_ms, 5), tflops=round(flops / (steady_ms * 1e-3) / 1e12, 2),
+                  frac=round(flops / (steady_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                  clock_mhz=[_clock_mhz(clk, 2), _clock_mhz(clk, 3)])
     return dict(cfg=cfg, wall_ms=wall_ms, kern_ms=kern_ms, flops=flops, exact_flops=cfg.flops(),
-                tflops_wall=flops / (wall_ms * 1e-3) / 1e12, tflops_kern=flops / (kern_ms * 1e-3) / 1e12)
+                tflops_wall=flops / (wall_ms * 1e-3) / 1e12, tflops_kern=flops / (kern_ms * 1e-3) / 1e12,
+                clock_mhz=[_clock_mhz(clk, 0), _clock_mhz(clk, 1)], steady=steady)
 
 
 def bench_decode(args, dev):
@@ -111,11 +147,28 @@ def bench_decode(args, dev):
     fn = lambda: A.decode_attention(q, kc, vc, splits=cfg.splits, out=out, workspace=ws)  # noqa: E731
     ms = _events_time(fn, max(5, args.steps // 2), 2)
     nbytes = cfg.bytes()
-    del kc, vc
+    del kc, vc, ws
     torch.cuda.empty_cache()
     gbps = nbytes / (ms * 1e-3) / 1e9
-    return dict(workload=cfg.name, ms=round(ms, 4), bytes=nbytes, gbps=round(gbps, 1),
-                frac=round(gbps / PEAK_HBM_GBPS, 4), splits=cfg.splits)
+    res = dict(workload=cfg.name, ms=round(ms, 4), bytes=nbytes, gbps=round(gbps, 1),
+               frac=round(gbps / PEAK_HBM_GBPS, 4), splits=cfg.splits)
+    # The same decode through the drop-in compile(Attn) callable: q [B, 1, H, D] and the cache in the case layout
+    # [B, L, H, D] (attn.py:18-34 with q_len == 1), routed to the split-KV kernels by attention().
+    from deepgengraph_amd import cases as tcases
+    from deepgengraph_amd.compile import compile as dgg_compile
+
+    qc = torch.randn(cfg.B, 1, cfg.Hq, cfg.D, device=dev).to(cfg.dtype)
+    kcl = torch.randn(cfg.B, cfg.L, cfg.Hkv, cfg.D, device=dev, dtype=cfg.dtype)
+    vcl = torch.randn(cfg.B, cfg.L, cfg.Hkv, cfg.D, device=dev, dtype=cfg.dtype)
+    model = tcases.Attn(kv_head_num=cfg.Hkv, head_num=cfg.Hq, head_dim=cfg.D)
+    f = dgg_compile(model, ["q", "k", "v"], [qc, kcl, vcl], ["out"], "mi355x")
+    ms = _events_time(lambda: f(qc, kcl, vcl), max(5, args.steps // 2), 2)
+    del kcl, vcl
+    torch.cuda.empty_cache()
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    res["compile_attn_case_layout"] = dict(ms=round(ms, 4), gbps=round(gbps, 1), frac=round(gbps / PEAK_HBM_GBPS, 4),
+                                           splits=A.decode_splits(cfg.B, cfg.Hq, cfg.L))
+    return res
 
 
 def bench_prestep(args, dev):
@@ -263,8 +316,8 @@ def cpu_baseline(target_s: float = 10.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=500)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--sections", default="prefill,decode,prestep,variants,block")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -309,6 +362,8 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(pre["tflops_kern"], 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(pre["tflops_kern"] / PEAK_BF16_TFLOPS, 4),
                      "traffic": measured_traffic("attn_fwd_dma_kernel<BF16, 128"), "kernel_ms": round(pre["kern_ms"], 5)},
+        "clock_mhz": pre["clock_mhz"],
+        "steady": pre["steady"],
     }
     line.update(extra)
     if not args.no_cpu_baseline:

@@ -30,6 +30,26 @@ def _check_qk(name: str, q: torch.Tensor, k: torch.Tensor):
         raise RuntimeError(f"{name}: q and k dtypes differ")
 
 
+# Key count from which a one-row call runs on the split-KV decode kernels instead of the prefill kernel (whose
+# 256-row workgroups would compute one live row per (batch, head)).
+DECODE_MIN_KEYS = 256
+
+
+def _decode_shaped(Sq: int, Sk: int, softcap, window, ref_rounding: bool, dtype) -> bool:
+    """A call the decode kernels compute exactly as the prefill kernel would: one query row (nothing masked by the
+    bottom-right causal mask), enough keys to split, no soft-cap, no window that hides keys, no reference
+    rounding (the decode kernels keep fp32 scores)."""
+    return (Sq == 1 and Sk >= DECODE_MIN_KEYS and not softcap and (not window or window >= Sk) and not ref_rounding
+            and dtype in (torch.float16, torch.bfloat16))
+
+
+def decode_splits(B: int, Hq: int, L: int) -> int:
+    """Split count for a decode call: at least ~2048 workgroups over the chip (8 per CU) when the cache allows,
+    and at least 128 keys per split (one unrolled block of the partial kernel)."""
+    want = -(-2048 // max(1, B * Hq))
+    return int(max(1, min(1024, want, -(-L // 128))))
+
+
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool = True, softcap: float = 0.0,
               window: int = 0, scale: float | None = None, return_lse: bool = False, ref_rounding: bool = False,
               out: torch.Tensor | None = None, lse_base2: bool = False):
@@ -41,7 +61,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool
     gemma2.py:19-38): scores = q.k^T * scale (default 1/sqrt(D)), optional softcap*tanh(scores/softcap),
     bottom-right aligned causal mask (attn.py:22-23), optional sliding window (key j visible iff
     i + Sk - Sq - j < window), fp32 softmax, P.V. ref_rounding rounds the scores to the input dtype at the
-    reference's rounding points (slower; used for H2O selection parity)."""
+    reference's rounding points (slower; used for H2O selection parity). A one-row call over at least
+    DECODE_MIN_KEYS keys (the reference's decode case) runs on the split-KV decode kernels."""
     dev = _lib.require_gpu(q, k, v, out)
     for name, t in (("q", q), ("k", k), ("v", v)):
         _check_bshd(name, t)
@@ -59,6 +80,20 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool
             raise RuntimeError("attention: out must match q in shape and dtype")
     lse = torch.empty(B, Hq, Sq, dtype=torch.float32, device=q.device) if return_lse else None
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    if _decode_shaped(Sq, Sk, softcap, window, ref_rounding, q.dtype):
+        # One query row (attn.py:22-23: the bottom-right causal mask hides nothing): the split-KV decode kernels,
+        # reading the case layout [B, L, H, D] through its strides.
+        splits = decode_splits(B, Hq, Sk)
+        ws = torch.empty(max(decode_workspace_bytes(B, Hq, D, splits), 16), dtype=torch.uint8, device=q.device)
+        lse1 = torch.empty(B, Hq, dtype=torch.float32, device=q.device) if return_lse else None
+        strides = _lib.int64_array([q.stride(0), q.stride(2), k.stride(0), k.stride(2), k.stride(1), v.stride(0),
+                                    v.stride(2), v.stride(1), out.stride(0), out.stride(2)])
+        _lib.call("dgg_attn_decode", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out), _lib.ptr(lse1),
+                  _lib.ptr(ws), ws.numel(), B, Hq, Hkv, Sk, D, strides, splits, scale, _lib.dtype_code(q.dtype),
+                  _lib.stream_handle(dev))
+        if return_lse:
+            lse.copy_(lse1.view(B, Hq, 1) * (math.log2(math.e) if lse_base2 else 1.0))
+        return (out, lse) if return_lse else out
     flags = ((_lib.ATTN_CAUSAL if causal else 0) | (_lib.ATTN_REF_ROUNDING if ref_rounding else 0)
              | (_lib.ATTN_LSE_BASE2 if lse_base2 else 0))
     strides = _lib.int64_array([*q.stride()[:3], *k.stride()[:3], *v.stride()[:3], *out.stride()[:3]])

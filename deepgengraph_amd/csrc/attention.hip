@@ -17,11 +17,11 @@
 // masked tiles dead 32-key blocks skip their MFMAs. attn_colsum_d128_kernel / attn_colsum_kernel recompute
 // P = exp2(s - lse) with one key per lane and sum (or test) it over the queries; attn_kf_rowlse_kernel is the
 // row pass of KeyFormer's perturbed softmax. Reference rounding (DGG_ATTN_REF_ROUNDING) rounds the scores as
-// the reference does, by the exact division sequence (mode 1) or a host-verified multiplier (mode 2).
+// the reference does on the GPU: matmul result to the input dtype, then the fp32 multiply by the reciprocal of
+// sqrt(D) (and of the soft-cap), rounded again.
 // Workgroups are ordered longest-first and grouped by head inside each XCD so the K/V of a head stay in one L2.
 #include <algorithm>
-#include <cstring>
-#include <mutex>
+#include <cmath>
 #include <type_traits>
 
 #include "common.h"
@@ -237,12 +237,13 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D
 
   // Full next tiles are prefetched into registers before this tile's compute; the ragged last tile (at most one)
   // is loaded after it.
+  const bool wave_live = q0 + 32 * w < p.Sq;  // wave-uniform: a wave past the end only stages tiles
   auto step = [&](const int t, auto masked) {
     const int buf = (t - t_begin) & 1;
     const int tn = t + 1;
     const bool prefetch = tn < t_end && tile_full(tn);
     if (prefetch) load_full();
-    tile(t, buf, masked);
+    if (wave_live) tile(t, buf, masked);
     if (tn < t_end) {
       if (!prefetch) load_ragged(tn);
       store_tile(buf ^ 1);
@@ -683,7 +684,7 @@ attn_fwd_dma_kernel(AttnParams p) {
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
-          for (int jp = 0; jp < 8; ++jp) hs[n][mb][jp] = ref_scores_f16<REFROUND>(sacc[n][mb][2 * jp], sacc[n][mb][2 * jp + 1], p);
+          for (int jp = 0; jp < 8; ++jp) hs[n][mb][jp] = ref_scores_f16(sacc[n][mb][2 * jp], sacc[n][mb][2 * jp + 1], p);
       }
       if constexpr (PKM) {
         f16x2 mx = hs[n][0][0];
@@ -793,8 +794,10 @@ attn_fwd_dma_kernel(AttnParams p) {
   }
   if (t_full1 > t_full0 && t_full1 * BN > p.Sk) t_full1 = max(t_full0, p.Sk / BN);
   if (t_full1 < t_full0) t_full1 = t_full0;
+  // A wave whose rows all lie past the end (qw0 >= Sq: the last workgroup of a ragged or short query range,
+  // e.g. a single decode-like row) computes no tile; it still issues its share of the copies and meets the barriers.
   const int wt_begin = wk_begin / BN;
-  const int wt_end = wk_end > wk_begin ? (wk_end + BN - 1) / BN : wt_begin;
+  const int wt_end = qw0 < p.Sq && wk_end > wk_begin ? (wk_end + BN - 1) / BN : wt_begin;
 
   // Pipeline: tiles t+1 .. t+NSTAGE-2 may still be in flight while tile t is waited for; the copy of tile
   // t+NSTAGE-1 is issued after the barrier into the stage that held tile t-1.
@@ -1166,7 +1169,7 @@ attn_colsum_d128_kernel(AttnParams p) {
       f16x2 hs[8];
       if constexpr (PK) {
 #pragma unroll
-        for (int jp = 0; jp < 8; ++jp) hs[jp] = ref_scores_f16<REFROUND>(sacc[mb][2 * jp], sacc[mb][2 * jp + 1], p);
+        for (int jp = 0; jp < 8; ++jp) hs[jp] = ref_scores_f16(sacc[mb][2 * jp], sacc[mb][2 * jp + 1], p);
       }
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
@@ -1274,22 +1277,12 @@ void launch_fwd_d256(const AttnParams& p, hipStream_t st) {
                        dim3(grid), dim3(64 * kD256NW), 0, st, p);
 }
 
-// Reference-rounding mode of a launch (the REFROUND template argument): 0 off, 1 the exact fp32 division
-// sequence (ref_quot), 2 one multiply by the host-verified ref_mul. Mode 2 is built for head_dim 128 without
-// soft-cap (the config-4 family: H2O, RoCo, SnapKV, Corm, KeyFormer); everything else uses mode 1.
+// Reference-rounding mode of a launch (the REFROUND template argument): 0 off, 1 the scores rounded as the
+// reference rounds them (score_value).
 template <int D, bool SOFTCAP, typename F>
 void with_ref_mode(bool ref, const AttnParams& p, F&& f) {
-  if (!ref) {
-    f(std::integral_constant<int, 0>{});
-    return;
-  }
-  if constexpr (D == 128 && !SOFTCAP) {
-    if (p.ref_mul_ok) {
-      f(std::integral_constant<int, 2>{});
-      return;
-    }
-  }
-  f(std::integral_constant<int, 1>{});
+  if (ref) f(std::integral_constant<int, 1>{});
+  else f(std::integral_constant<int, 0>{});
 }
 
 template <typename T, int D, bool MASK, bool SOFTCAP>
@@ -1382,8 +1375,8 @@ void pick_kf_rowlse(const AttnParams& p, bool ref, bool vec, hipStream_t st) {
 int validate_attn(const char* op, const void* q, const void* k, int64_t B, int64_t Sq, int64_t Sk, int64_t Hq,
                   int64_t Hkv, int64_t D, const int64_t* strides, int nstrides, float scale, float softcap,
                   int64_t window, int dtype) {
-  DGG_REQUIRE(dtype == DGG_F16 || dtype == DGG_BF16, DGG_ERR_DTYPE,
-              "%s: dtype code %d not supported (attention kernels take f16 or bf16)", op, dtype);
+  DGG_REQUIRE(dtype == DGG_F16 || dtype == DGG_BF16 || dtype == DGG_F32, DGG_ERR_DTYPE,
+              "%s: dtype code %d not supported (attention kernels take f32, f16 or bf16)", op, dtype);
   DGG_REQUIRE(D == 64 || D == 128 || D == 256, DGG_ERR_UNSUPPORTED, "%s: head_dim %lld not supported (64, 128, 256)",
               op, (long long)D);
   DGG_REQUIRE(B >= 0 && Sq >= 0 && Sk >= 0, DGG_ERR_SHAPE, "%s: negative size", op);
@@ -1404,118 +1397,21 @@ int validate_attn(const char* op, const void* q, const void* k, int64_t B, int64
   DGG_REQUIRE(std::isfinite(scale) && scale > 0.f, DGG_ERR_SHAPE, "%s: scale must be finite and > 0", op);
   DGG_REQUIRE(softcap >= 0.f && std::isfinite(softcap), DGG_ERR_SHAPE, "%s: softcap must be >= 0 (0 = off)", op);
   DGG_REQUIRE(window >= 0 && window < (1ll << 30), DGG_ERR_SHAPE, "%s: window must be >= 0 (0 = off)", op);
-  if (B == 0 || Sq == 0 || Sk == 0) return DGG_OK;
-  DGG_REQUIRE(q && k, DGG_ERR_NULL, "%s: null q/k pointer", op);
-  DGG_REQUIRE(dgg::aligned16(q) && dgg::aligned16(k), DGG_ERR_ALIGN, "%s: q/k must be 16-byte aligned", op);
+  // q is read whenever there are query rows (the forward kernels load it even when Sk == 0), k whenever there are
+  // keys.
+  if (B > 0 && Sq > 0) {
+    DGG_REQUIRE(q != nullptr, DGG_ERR_NULL, "%s: null q pointer", op);
+    DGG_REQUIRE(dgg::aligned16(q), DGG_ERR_ALIGN, "%s: q must be 16-byte aligned", op);
+  }
+  if (B > 0 && Sk > 0) {
+    DGG_REQUIRE(k != nullptr, DGG_ERR_NULL, "%s: null k pointer", op);
+    DGG_REQUIRE(dgg::aligned16(k), DGG_ERR_ALIGN, "%s: k must be 16-byte aligned", op);
+  }
   return DGG_OK;
 }
 
-// 16-bit rounding (to nearest even, overflow to infinity) of an fp32 value, as bit patterns.
-uint16_t rn_f16_bits(float f) {
-  uint32_t x;
-  std::memcpy(&x, &f, 4);
-  const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
-  if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);   // NaN
-  if (ax >= 0x47800000u) return (uint16_t)(sign | 0x7c00u);  // >= 2^16 (and inf): infinity
-  if (ax < 0x38800000u) {                                     // below 2^-14: subnormal result in units of 2^-24
-    float a;
-    std::memcpy(&a, &ax, 4);
-    return (uint16_t)(sign | (uint32_t)std::nearbyint(a * 16777216.0f));
-  }
-  uint32_t h = ((((ax >> 23) - 112u) << 10) | ((ax & 0x7fffffu) >> 13));
-  const uint32_t rem = ax & 0x1fffu;
-  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;  // a carry moves into the exponent (65520.. -> inf)
-  return (uint16_t)(sign | h);
-}
-uint16_t rn_bf16_bits(float f) {
-  uint32_t x;
-  std::memcpy(&x, &f, 4);
-  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
-  return (uint16_t)((x + 0x7fffu + ((x >> 16) & 1u)) >> 16);
-}
-float f16_bits_value(uint16_t h) {
-  const int e = (h >> 10) & 31, m = h & 1023;
-  const float mag = e == 0 ? std::ldexp((float)m, -24) : e == 31 ? (m ? NAN : INFINITY) : std::ldexp((float)(1024 + m), e - 25);
-  return (h & 0x8000u) ? -mag : mag;
-}
-
-// The reference divides each 16-bit score x by d in fp32 and rounds the quotient back to 16 bits
-// (attn.py:29, h2o.py:29). Looks for an fp32 multiplier y with RN16(RN32(x * y)) == RN16(RN32(x / d)) for every
-// finite 16-bit x (signed zeros equal), trying RN(1/d) and then the fp32 values up to 4 ulps around it; the
-// kernels then replace the division sequence by one multiply (reference-rounding mode 2). The exhaustive check
-// runs once per (dtype, d); results are cached.
-bool ref_multiplier(int dtype, float d, float* y_out) {
-  struct Entry {
-    int dtype;
-    uint32_t dbits;
-    bool ok;
-    float y;
-  };
-  static std::mutex mu;
-  static Entry cache[32];
-  static int n_cache = 0;
-  uint32_t dbits;
-  std::memcpy(&dbits, &d, 4);
-  {
-    std::lock_guard<std::mutex> lock(mu);
-    for (int i = 0; i < n_cache; ++i)
-      if (cache[i].dtype == dtype && cache[i].dbits == dbits) {
-        *y_out = cache[i].y;
-        return cache[i].ok;
-      }
-  }
-  const bool f16 = dtype == DGG_F16;
-  auto rn = [&](float v) { return f16 ? rn_f16_bits(v) : rn_bf16_bits(v); };
-  auto works = [&](float y) {
-    for (uint32_t b = 0; b < 65536u; ++b) {
-      float x;
-      if (f16) {
-        x = f16_bits_value((uint16_t)b);
-      } else {
-        const uint32_t xb = b << 16;
-        std::memcpy(&x, &xb, 4);
-      }
-      if (!std::isfinite(x)) continue;
-      const uint16_t want = rn(x / d), got = rn(x * y);
-      if (want != got && ((want | got) & 0x7fffu) != 0) return false;
-    }
-    return true;
-  };
-  const float y0 = 1.0f / d;
-  float cand[9] = {y0};
-  float up = y0, down = y0;
-  for (int i = 1; i <= 4; ++i) {
-    up = std::nextafter(up, INFINITY);
-    down = std::nextafter(down, 0.0f);
-    cand[2 * i - 1] = up;
-    cand[2 * i] = down;
-  }
-  bool ok = false;
-  float y = y0;
-  if (std::isfinite(d) && d > 0.f && std::isfinite(y0) && y0 > 0.f)
-    for (float c : cand)
-      if (works(c)) {
-        ok = true;
-        y = c;
-        break;
-      }
-  {
-    std::lock_guard<std::mutex> lock(mu);
-    if (n_cache < 32) cache[n_cache++] = Entry{dtype, dbits, ok, y};
-  }
-  *y_out = y;
-  return ok;
-}
-
-// Reference-rounding parameters of a launch: the verified multiplier when reference rounding is on.
-void set_ref_mode(AttnParams& p, uint32_t flags, int dtype) {
-  p.ref_mul = p.ref_rcp;
-  p.ref_mul_ok = 0;
-  if (flags & DGG_ATTN_REF_ROUNDING) p.ref_mul_ok = ref_multiplier(dtype, p.ref_div, &p.ref_mul) ? 1 : 0;
-}
-
 AttnParams make_params(const void* q, const void* k, const void* v, void* o, int64_t B, int64_t Sq, int64_t Sk,
-                       int64_t Hq, int64_t Hkv, float scale, float softcap, int64_t window, uint32_t flags) {
+                       int64_t Hq, int64_t Hkv, int64_t D, float scale, float softcap, int64_t window, uint32_t flags) {
   AttnParams p{};
   p.q = q;
   p.k = k;
@@ -1532,7 +1428,10 @@ AttnParams make_params(const void* q, const void* k, const void* v, void* o, int
   p.window = (int)window;
   p.offset = (int)(Sk - Sq);
   p.scale = scale;
-  p.ref_div = (float)(1.0 / (double)scale);
+  // The reference divides its scores by math.sqrt(D) (attn.py:29); torch takes that Python float to fp32 and
+  // multiplies by the fp32 reciprocal. A scale other than the default is taken as 1 / divisor.
+  const double root = std::sqrt((double)D);
+  p.ref_div = scale == (float)(1.0 / root) ? (float)root : (float)(1.0 / (double)scale);
   p.ref_rcp = 1.0f / p.ref_div;
   p.c_fast = scale * kLog2e;
   p.softcap = softcap;
@@ -1544,13 +1443,6 @@ AttnParams make_params(const void* q, const void* k, const void* v, void* o, int
 
 }  // namespace
 
-extern "C" int dgg_ref_multiplier(int dtype, float d, float* y) {
-  DGG_REQUIRE(dtype == DGG_F16 || dtype == DGG_BF16, DGG_ERR_DTYPE, "ref_multiplier: dtype code %d not f16/bf16",
-              dtype);
-  DGG_REQUIRE(y != nullptr, DGG_ERR_NULL, "ref_multiplier: null output pointer");
-  return ref_multiplier(dtype, d, y) ? 1 : 0;
-}
-
 extern "C" int dgg_attn_prefill(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B,
                                 int64_t Sq, int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides,
                                 float scale, float softcap, int64_t window, uint32_t flags, int dtype, void* stream) {
@@ -1559,8 +1451,7 @@ extern "C" int dgg_attn_prefill(const void* q, const void* k, const void* v, voi
   if (B == 0 || Sq == 0) return DGG_OK;
   DGG_REQUIRE(o && (v || Sk == 0), DGG_ERR_NULL, "attn_prefill: null v/o pointer");
   DGG_REQUIRE(dgg::aligned16(v) && dgg::aligned16(o), DGG_ERR_ALIGN, "attn_prefill: v/o must be 16-byte aligned");
-  AttnParams p = make_params(q, k, v, o, B, Sq, Sk, Hq, Hkv, scale, softcap, window, flags);
-  set_ref_mode(p, flags, dtype);
+  AttnParams p = make_params(q, k, v, o, B, Sq, Sk, Hq, Hkv, D, scale, softcap, window, flags);
   p.lse = lse;
   p.q_sb = strides[0]; p.q_ss = strides[1]; p.q_sh = strides[2];
   p.k_sb = strides[3]; p.k_ss = strides[4]; p.k_sh = strides[5];
@@ -1569,6 +1460,11 @@ extern "C" int dgg_attn_prefill(const void* q, const void* k, const void* v, voi
   const bool ref = (flags & DGG_ATTN_REF_ROUNDING) != 0;
   hipStream_t st = dgg::as_stream(stream);
   // Sk == 0 still launches and writes o = 0 (the reference's P.V over an empty key axis) and lse = -inf.
+  if (dtype == DGG_F32) {  // fp32 has no 16-bit rounding point: reference rounding changes nothing
+    p.n_tiles = (int)((Sq + f32_rows_per_tile() - 1) / f32_rows_per_tile());
+    launch_attn_f32_fwd(p, (int)D, st);
+    return dgg::check_launch("attn_prefill");
+  }
   const int64_t bm = D == 128 ? kD128BM : D == 256 ? kD256BM : kBM;
   p.n_tiles = (int)((Sq + bm - 1) / bm);
   if (dtype == DGG_BF16) {
@@ -1603,8 +1499,7 @@ int colscore(const char* op, const void* q, const void* k, const float* lse, int
     DGG_REQUIRE(out0 != nullptr && (epi != kColSumSq || out1 != nullptr), DGG_ERR_NULL, "%s: null output pointer", op);
   }
   DGG_REQUIRE(Sq == 0 || lse != nullptr, DGG_ERR_NULL, "%s: null lse pointer", op);
-  AttnParams p = make_params(q, k, nullptr, nullptr, B, Sq, Sk, Hq, Hkv, scale, softcap, window, flags);
-  set_ref_mode(p, flags, dtype);
+  AttnParams p = make_params(q, k, nullptr, nullptr, B, Sq, Sk, Hq, Hkv, D, scale, softcap, window, flags);
   p.lse = const_cast<float*>(lse);
   p.colsum = out0;
   p.colsum2 = out1;
@@ -1613,10 +1508,15 @@ int colscore(const char* op, const void* q, const void* k, const float* lse, int
   p.thr_rs = thr_row_stride;
   p.q_sb = strides[0]; p.q_ss = strides[1]; p.q_sh = strides[2];
   p.k_sb = strides[3]; p.k_ss = strides[4]; p.k_sh = strides[5];
+  hipStream_t st = dgg::as_stream(stream);
+  if (dtype == DGG_F32) {
+    p.n_tiles = (int)((Sk + f32_rows_per_tile() - 1) / f32_rows_per_tile());
+    launch_attn_f32_col(p, (int)D, epi, st);
+    return dgg::check_launch(op);
+  }
   const int64_t bk = D == 128 ? kC128BK : kCBK;
   p.n_tiles = (int)((Sk + bk - 1) / bk);
   const bool ref = (flags & DGG_ATTN_REF_ROUNDING) != 0;
-  hipStream_t st = dgg::as_stream(stream);
   if (dtype == DGG_BF16) {
     if (D == 64) pick_col<BF16, 64>(p, ref, epi, st);
     else if (D == 128) pick_col<BF16, 128>(p, ref, epi, st);
@@ -1657,13 +1557,14 @@ extern "C" int dgg_attn_kf_rowlse(const void* q, const void* k, const float* exp
                                   const int64_t* strides, float scale, float tau, int64_t window, uint32_t flags,
                                   int dtype, void* stream) {
   const char* op = "attn_kf_rowlse";
+  DGG_REQUIRE(dtype == DGG_F16 || dtype == DGG_BF16, DGG_ERR_DTYPE,
+              "%s: dtype code %d not supported (the KeyFormer passes take f16 or bf16)", op, dtype);
   if (int rc = validate_attn(op, q, k, B, Sq, Sk, Hq, Hkv, D, strides, 6, scale, 0.f, window, dtype)) return rc;
   if (B == 0 || Sq == 0) return DGG_OK;
   DGG_REQUIRE(lse2 != nullptr, DGG_ERR_NULL, "%s: null lse output", op);
   DGG_REQUIRE(Sk > 0, DGG_ERR_SHAPE, "%s: Sk must be > 0", op);
   if (int rc = validate_exp_rand(op, exp_rand, er_strides, Sq, tau)) return rc;
-  AttnParams p = make_params(q, k, nullptr, nullptr, B, Sq, Sk, Hq, Hkv, scale, 0.f, window, flags);
-  set_ref_mode(p, flags, dtype);
+  AttnParams p = make_params(q, k, nullptr, nullptr, B, Sq, Sk, Hq, Hkv, D, scale, 0.f, window, flags);
   p.lse = lse2;
   p.q_sb = strides[0]; p.q_ss = strides[1]; p.q_sh = strides[2];
   p.k_sb = strides[3]; p.k_ss = strides[4]; p.k_sh = strides[5];
@@ -1689,6 +1590,8 @@ extern "C" int dgg_attn_kf_colsum(const void* q, const void* k, const float* exp
                                   int64_t Hkv, int64_t D, const int64_t* strides, float scale, float tau,
                                   int64_t window, uint32_t flags, int dtype, void* stream) {
   const char* op = "attn_kf_colsum";
+  DGG_REQUIRE(dtype == DGG_F16 || dtype == DGG_BF16, DGG_ERR_DTYPE,
+              "%s: dtype code %d not supported (the KeyFormer passes take f16 or bf16)", op, dtype);
   if (int rc = validate_attn(op, q, k, B, Sq, Sk, Hq, Hkv, D, strides, 6, scale, 0.f, window, dtype)) return rc;
   if (B == 0 || Sk == 0) return DGG_OK;
   DGG_REQUIRE(kf_score != nullptr, DGG_ERR_NULL, "%s: null output", op);
@@ -1696,9 +1599,8 @@ extern "C" int dgg_attn_kf_colsum(const void* q, const void* k, const float* exp
   if (Sq > 0)
     if (int rc = validate_exp_rand(op, exp_rand, er_strides, Sq, tau)) return rc;
   // The row lse of the perturbed scores is base 2 (as dgg_attn_kf_rowlse writes it).
-  AttnParams p = make_params(q, k, nullptr, nullptr, B, Sq, Sk, Hq, Hkv, scale, 0.f, window,
+  AttnParams p = make_params(q, k, nullptr, nullptr, B, Sq, Sk, Hq, Hkv, D, scale, 0.f, window,
                              flags | DGG_ATTN_LSE_BASE2);
-  set_ref_mode(p, flags, dtype);
   p.lse = const_cast<float*>(lse2);
   p.colsum = kf_score;
   p.q_sb = strides[0]; p.q_ss = strides[1]; p.q_sh = strides[2];

@@ -42,11 +42,8 @@ struct AttnParams {
   int offset;    // Sk - Sq (bottom-right aligned causal mask)
   int lse_base2;  // lse written / read in base 2 (DGG_ATTN_LSE_BASE2)
   float scale;
-  float ref_div;  // 1 / scale rounded to fp32 (== fp32 sqrt(D) for the usual scale): the reference divides
-                  // the rounded scores by it
-  float ref_rcp;  // 1 / ref_div rounded to fp32
-  float ref_mul;  // fp32 multiplier with RN16(x * ref_mul) == RN16(x / ref_div) for every finite 16-bit x
-  int ref_mul_ok; // ref_mul verified on the host for this dtype (reference rounding mode 2)
+  float ref_div;  // the divisor of the reference's scores, fp32: sqrt(D) for the default scale, else 1 / scale
+  float ref_rcp;  // RN32(1 / ref_div): torch on the GPU divides a tensor by a Python scalar as x * this
   float c_fast;  // scale * log2(e): converts raw scores to the exp2 domain
   float inv_softcap;
   float softcap;
@@ -84,36 +81,21 @@ __device__ __forceinline__ float round_t(float x) {
   return to_f<typename T::scalar>(to_s<typename T::scalar>(x));
 }
 
-// x / d for the reference-rounding mode, from y = RN(1/d): q = RN(x*y), r = x - q*d (exact in one fma),
-// q' = RN(q + r*y). By Markstein's theorem (y within half an ulp of 1/d, q within one ulp of x/d) q' is the
-// correctly rounded quotient RN(x/d) whenever no intermediate underflows or overflows. Every caller rounds
-// q' on to fp16 / bf16 at once; checked exhaustively over all 2^16 fp16 and bf16 x for the usual divisors
-// and 200 random ones in [0.01, 1000] (tests/test_ref_division.py), the rounded results equal those of the
-// true division (up to the sign of a zero quotient, which no later step sees). The clamp keeps x = +-inf (a
-// score that overflowed fp16) from turning into inf - inf: it yields +-inf like the division does. Three
-// fma-class instructions and a clamp instead of the ~10 of the IEEE division sequence.
-__device__ __forceinline__ float ref_quot(float x, float d, float y) {
-  float q = fmaf(x, y, 0.0f);  // +0 addend keeps v_fma_mix (a -0 addend folds to a plain multiply)
-  q = __builtin_amdgcn_fmed3f(q, -3.402823466e38f, 3.402823466e38f);
-  const float r = fmaf(-q, d, x);
-  return fmaf(r, y, q);
-}
-
 // Score transform shared by the forward and column-sum kernels. Returns the value whose exp2 (after the
 // row maximum / lse is subtracted and `c` applied) is the unnormalised probability:
 //   fast path (no soft-cap, no reference rounding): the raw fp32 score; the caller multiplies by c_fast.
 //   otherwise: the score already in the exp2 domain (c = 1).
-// REFROUND: 0 off; 1 the division by ref_div as the exact sequence above; 2 one multiply by ref_mul, which the host
-// verified to give the same 16-bit result for every finite 16-bit input.
+// REFROUND: the scores are rounded to the input dtype where the reference rounds them (attn.py:29,
+// gemma2.py:29-33). Each division by a Python float there (`/ math.sqrt(D)`, `/= softcap`) is what torch executes
+// on the GPU for a tensor divided by a CPU scalar: one fp32 multiply by the fp32 reciprocal of the divisor, then
+// the rounding to the tensor dtype.
 template <typename T, bool SOFTCAP, int REFROUND>
 __device__ __forceinline__ float score_value(float s, const AttnParams& p) {
   if constexpr (REFROUND) {
-    // deepgengraph_exp/cases/kernels/attn.py:29 / gemma2.py:29-33: each step rounded to the input dtype;
-    // `/ math.sqrt(D)` is an fp32 true division before the rounding.
     s = round_t<T>(s);
-    s = round_t<T>(REFROUND == 2 ? fmaf(s, p.ref_mul, 0.0f) : ref_quot(s, p.ref_div, p.ref_rcp));
+    s = round_t<T>(s * p.ref_rcp);
     if constexpr (SOFTCAP) {
-      s = round_t<T>(ref_quot(s, p.softcap, p.inv_softcap));
+      s = round_t<T>(s * p.inv_softcap);
       s = round_t<T>(tanhf(s));
       s = round_t<T>(s * p.softcap);
     }
@@ -167,14 +149,13 @@ struct ColAcc {
 };
 
 // Reference-rounded fp16 scores of two raw fp32 dot products, kept packed (natural-log domain): the matmul
-// output rounded to fp16, divided by ref_div, rounded again (attn.py:29 / h2o.py:29). The conversions are
-// v_cvt_pk_f16_f32 and the fp16 operands feed v_fma_mix_f32 directly, so the pair costs ten instructions with
-// the division sequence (REFROUND 1) and four with the verified multiplier (REFROUND 2).
-template <int REFROUND>
+// output rounded to fp16, multiplied by the fp32 reciprocal of the divisor, rounded again (attn.py:29 /
+// h2o.py:29 as torch runs them on the GPU). The conversions are v_cvt_pk_f16_f32 and the fp16 operands feed
+// v_fma_mix_f32 directly: four instructions per pair.
 __device__ __forceinline__ f16x2 ref_scores_f16(float a, float b, const AttnParams& p) {
   const f16x2 h = __builtin_convertvector(f32x2{a, b}, f16x2);
-  const float q0 = REFROUND == 2 ? fmaf((float)h[0], p.ref_mul, 0.0f) : ref_quot((float)h[0], p.ref_div, p.ref_rcp);
-  const float q1 = REFROUND == 2 ? fmaf((float)h[1], p.ref_mul, 0.0f) : ref_quot((float)h[1], p.ref_div, p.ref_rcp);
+  const float q0 = fmaf((float)h[0], p.ref_rcp, 0.0f);  // +0 addend keeps v_fma_mix (exact: RN32(x * y))
+  const float q1 = fmaf((float)h[1], p.ref_rcp, 0.0f);
   return __builtin_convertvector(f32x2{q0, q1}, f16x2);
 }
 
@@ -272,5 +253,10 @@ __device__ __forceinline__ float rowsum8(f16x8 v, float l) {
   return __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 6, 7), one, l, false);
 }
 
+
+// fp32 inputs (attention_f32.hip): the forward and the column-score pass, rows per workgroup tile of both.
+int f32_rows_per_tile();
+void launch_attn_f32_fwd(const AttnParams& p, int D, hipStream_t st);
+void launch_attn_f32_col(const AttnParams& p, int D, int epi, hipStream_t st);
 
 }  // namespace dgg_attn

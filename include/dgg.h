@@ -40,8 +40,10 @@ enum dgg_status {
 /* Flags for the attention entry points. */
 #define DGG_ATTN_CAUSAL 0x1u /* bottom-right aligned causal mask: key j is visible to query i iff j <= i + (Sk - Sq) */
 /* Round scores to the input dtype at the points where the reference's eager module rounds them
- * (Q.K^T result, the 1/sqrt(D) scaling, each soft-cap step) before the fp32 softmax. Costs a few VALU
- * ops per score; used where downstream selection (H2O top-k) depends on exact probabilities. */
+ * (Q.K^T result, the 1/sqrt(D) scaling, each soft-cap step) before the fp32 softmax. Each division by a
+ * Python float there is evaluated as torch does on the GPU: an fp32 multiply by the fp32 reciprocal of the
+ * fp32 divisor (sqrt(D) for the default scale, else 1 / scale; the soft-cap), rounded to the dtype. Costs a
+ * few VALU ops per score; used where downstream selection (H2O top-k) depends on exact probabilities. */
 #define DGG_ATTN_REF_ROUNDING 0x2u
 /* lse in base 2 (log2 of the row sum of 2^(scores*log2(e)), i.e. the natural lse times log2(e)):
  * dgg_attn_prefill writes it so and dgg_attn_colsum reads it so. Saves one multiply per score in the
@@ -170,14 +172,6 @@ int64_t dgg_nonzero_workspace_bytes(int64_t rows);
 int dgg_nonzero(const uint8_t* in, int ndim, const int64_t* dims, int64_t* coords, int64_t max_out, int64_t* total,
                 void* workspace, int64_t workspace_bytes, void* stream);
 
-/* Host-side check behind DGG_ATTN_REF_ROUNDING (no counterpart in the reference: the reference divides in fp32,
- * attn.py:29). Writes to *y an fp32 multiplier with RN16(RN32(x * y)) == RN16(RN32(x / d)) for every finite
- * 16-bit x of dtype (f16 or bf16; signed zeros equal) and returns 1, trying RN(1/d) and the 8 fp32 values
- * nearest it; returns 0 (and *y = RN(1/d)) when none qualifies. The attention entry points call it for
- * d = 1/scale and, when it succeeds at head_dim 128 without soft-cap, round scores with one multiply instead of
- * the division sequence. The result is cached per (dtype, d); the first call costs a few milliseconds. */
-int dgg_ref_multiplier(int dtype, float d, float* y);
-
 /* Top-k of H2O scores (deepgengraph_exp/cases/models/h2o.py:51-52: torch.topk then sort of the indices):
  * for each of `rows` rows of n fp32 scores (row stride n), the k largest, ties broken by the lowest index,
  * written as int64 indices in ascending index order to out_idx [rows, k]. -0.0 equals +0.0; NaN is not
@@ -194,6 +188,12 @@ int64_t dgg_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_
 int dgg_attn_decode(const void* q, const void* k, const void* v, void* o, float* lse, void* workspace,
                     int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
                     const int64_t* strides, int64_t splits, float scale, int dtype, void* stream);
+
+/* Shader-clock probe (no counterpart in the reference: measurement support for the benchmark). One lane spins for
+ * `ticks` ticks of the constant 100 MHz real-time counter and writes out[0] = shader cycles elapsed (s_memtime),
+ * out[1] = real-time ticks elapsed: the shader clock is out[0] / out[1] * 100 MHz. out: 2 device uint64, 8-byte
+ * aligned. ticks in [1, 10^6]. */
+int dgg_clock_probe(unsigned long long* out, int64_t ticks, void* stream);
 
 #ifdef __cplusplus
 }

@@ -5,6 +5,11 @@ evaluate the reference's eager PyTorch formula with its rounding points:
 
   scores = (q @ k^T) / sqrt(D)          in the input dtype (matmul result rounded, then the division rounded)
   soft-cap: scores /= c; tanh; *= c     each step in the input dtype (gemma2.py:31-33)
+
+Each division by a Python float is evaluated as torch evaluates it on the GPU the reference runs on: an fp32
+multiply by the fp32 reciprocal of the fp32 divisor, rounded to the tensor dtype (div_scalar). torch's CPU kernel
+divides instead; the two differ in the last bit of some 16-bit quotients (52 of the finite fp16 values at
+d = sqrt(128)), which can move a key across the H2O top-k boundary.
   scores += mask                        -inf / 0 in the input dtype; adding 0 is exact, so masked_fill is used
   probs = softmax(scores.float())       fp32
   out = probs.to(dtype) @ v             input dtype
@@ -17,6 +22,26 @@ import math
 
 import numpy as np
 import torch
+
+
+def div_scalar(x: torch.Tensor, d: float) -> torch.Tensor:
+    """x / d for a tensor x and a Python float d, as torch computes it on the GPU (the reference's
+    `torch.matmul(q, k^T) / math.sqrt(D)`, attn.py:29, and `scores /= softcap`, gemma2.py:31): the divisor is
+    taken to fp32, its reciprocal rounded to fp32, and x (in fp32) multiplied by it; the product is rounded to
+    x's dtype."""
+    inv = np.float32(1.0) / np.float32(d)
+    return (x.float() * float(inv)).to(x.dtype)
+
+
+def _scores(qt: torch.Tensor, kT: torch.Tensor, D: int, softcap=None) -> torch.Tensor:
+    """attn.py:29 / gemma2.py:29-33 in the input dtype: the matmul result rounded, divided by sqrt(D) (rounded),
+    and with a soft-cap: divided by it, tanh, multiplied by it, each rounded."""
+    scores = div_scalar(torch.matmul(qt, kT), math.sqrt(D))
+    if softcap:
+        scores = div_scalar(scores, softcap)
+        scores = torch.tanh(scores)
+        scores = scores * softcap
+    return scores
 
 
 def _mask(i0: int, n: int, Sq: int, Sk: int, causal: bool, window: int | None) -> torch.Tensor | None:
@@ -62,11 +87,7 @@ def attention(q, k, v, *, causal=True, softcap=None, window=None, return_lse=Fal
     lse = torch.empty(B, Hq, Sq, dtype=torch.float32) if return_lse else None
     for i0 in range(0, Sq, q_chunk):
         n = min(q_chunk, Sq - i0)
-        scores = torch.matmul(qt[:, :, i0:i0 + n], kT) / math.sqrt(D)  # attn.py:29
-        if softcap:
-            scores /= softcap  # gemma2.py:31-33
-            scores = torch.tanh(scores)
-            scores *= softcap
+        scores = _scores(qt[:, :, i0:i0 + n], kT, D, softcap)  # attn.py:29, gemma2.py:29-33
         hidden = _mask(i0, n, Sq, Sk, causal, window)
         if hidden is not None:
             scores = scores.masked_fill(hidden, float("-inf"))  # attn.py:30 (`scores += mask`)
@@ -94,7 +115,7 @@ def h2o(q, k, v, *, q_chunk=256):
     colsum = torch.zeros(B, Hq, Sk, dtype=torch.float32)
     for i0 in range(0, Sq, q_chunk):
         n = min(q_chunk, Sq - i0)
-        scores = torch.matmul(qt[:, :, i0:i0 + n], kT) / math.sqrt(D)  # h2o.py:29
+        scores = _scores(qt[:, :, i0:i0 + n], kT, D)  # h2o.py:29
         scores = scores.masked_fill(_mask(i0, n, Sq, Sk, True, None), float("-inf"))  # h2o.py:30
         sf = scores.float()
         probs = torch.softmax(sf, dim=-1)  # h2o.py:31
@@ -120,7 +141,7 @@ def _causal_probs(q, k, v, q_chunk):
     def gen():
         for i0 in range(0, Sq, q_chunk):
             n = min(q_chunk, Sq - i0)
-            scores = torch.matmul(qt[:, :, i0:i0 + n], kT) / math.sqrt(D)  # roco.py:37 / snapkv.py:31 / corm.py:30
+            scores = _scores(qt[:, :, i0:i0 + n], kT, D)  # roco.py:37 / snapkv.py:31 / corm.py:30
             scores = scores.masked_fill(_mask(i0, n, Sq, Sk, True, None), float("-inf"))
             sf = scores.float()
             probs = torch.softmax(sf, dim=-1)
@@ -188,7 +209,7 @@ def keyformer(q, k, v, exp_rand, *, tau=1.5, q_chunk=256):
     lse2p = torch.empty(B, H, Sq, dtype=torch.float32)
     for i0 in range(0, Sq, q_chunk):
         n = min(q_chunk, Sq - i0)
-        scores = torch.matmul(qt[:, :, i0:i0 + n], kT) / math.sqrt(D)  # kf.py:29
+        scores = _scores(qt[:, :, i0:i0 + n], kT, D)  # kf.py:29
         scores = scores.masked_fill(_mask(i0, n, Sq, Sk, True, None), float("-inf"))  # kf.py:30
         probs = torch.softmax(scores.float(), dim=-1)  # kf.py:31
         out[:, :, i0:i0 + n] = torch.matmul(probs.to(dt), vt)  # kf.py:32
@@ -228,7 +249,7 @@ def decode(q, k_cache, v_cache):
         if group > 1:
             kb = kb.repeat_interleave(group, dim=0)
             vb = vb.repeat_interleave(group, dim=0)
-        scores = torch.matmul(q[b].unsqueeze(1), kb.transpose(-2, -1)) / math.sqrt(D)  # [Hq, 1, L]
+        scores = _scores(q[b].unsqueeze(1), kb.transpose(-2, -1), D)  # [Hq, 1, L], attn.py:29
         sf = scores.float()
         probs = torch.softmax(sf, dim=-1)
         out[b] = torch.matmul(probs.to(dt), vb).squeeze(1)

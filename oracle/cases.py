@@ -24,11 +24,13 @@ class _Case(nn.Module):
         self.group_size = self.head_num // self.kv_head_num
 
     def prepare(self, batch_size=1, q_len=4096, kv_len=4096, dtype=torch.float16, device="cpu", seed=0):
-        """attn.py:36-50 / gemma2.py:41-54 / h2o.py:41-55, with randn inputs from a seeded CPU generator."""
+        """attn.py:36-50 / gemma2.py:41-54 / h2o.py:41-55 from a seeded CPU generator: Attn draws uniform [0, 1)
+        inputs (torch.rand, attn.py:38), the other cases N(0, 1) (torch.randn, gemma2.py:42)."""
         g = torch.Generator().manual_seed(seed)
-        q = torch.randn(batch_size, q_len, self.head_num, self.head_dim, generator=g).to(dtype).to(device)
-        k = torch.randn(batch_size, kv_len, self.kv_head_num, self.head_dim, generator=g).to(dtype).to(device)
-        v = torch.randn(batch_size, kv_len, self.kv_head_num, self.head_dim, generator=g).to(dtype).to(device)
+        draw = torch.rand if isinstance(self, Attn) else torch.randn
+        q = draw(batch_size, q_len, self.head_num, self.head_dim, generator=g).to(dtype).to(device)
+        k = draw(batch_size, kv_len, self.kv_head_num, self.head_dim, generator=g).to(dtype).to(device)
+        v = draw(batch_size, kv_len, self.kv_head_num, self.head_dim, generator=g).to(dtype).to(device)
         return {"input": {"q": q, "k": k, "v": v}, "output": list(self.OUTPUTS)}
 
 

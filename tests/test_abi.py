@@ -66,9 +66,8 @@ def _prefill(lib, **kw):
 
 
 def test_prefill_validation(lib):
-    assert _prefill(lib, dtype=_lib.DGG_F32) == E_DTYPE
-    assert b"f16 or bf16" in lib.dgg_last_error()
     assert _prefill(lib, dtype=7) == E_DTYPE
+    assert b"f32, f16 or bf16" in lib.dgg_last_error()
     assert _prefill(lib, D=96) == E_UNSUP
     assert _prefill(lib, Hq=3) == E_SHAPE
     assert _prefill(lib, B=-1) == E_SHAPE
@@ -83,6 +82,11 @@ def test_prefill_validation(lib):
     assert _prefill(lib, o=MIS) == E_ALIGN
     assert _prefill(lib, B=0) == OK  # empty: nothing to launch
     assert _prefill(lib, Sq=0) == OK
+    # no keys: the kernels still read q (and write o = 0), so q and o are checked whatever Sk is
+    assert _prefill(lib, Sk=0, q=None) == E_NULL
+    assert _prefill(lib, Sk=0, q=MIS) == E_ALIGN
+    assert _prefill(lib, Sk=0, o=None) == E_NULL
+    assert _prefill(lib, Sk=0, k=None, v=None, q=None) == E_NULL
 
 
 def test_colsum_validation(lib):
@@ -93,6 +97,20 @@ def test_colsum_validation(lib):
                                None) == E_NULL
     assert lib.dgg_attn_colsum(FAKE, FAKE, FAKE, FAKE, 1, 64, 64, 2, 2, 32, s, 0.1, 0.0, 0, 1, _lib.DGG_F16,
                                None) == E_UNSUP
+
+
+def test_keyformer_validation(lib):
+    s = _strides([128 * 512, 512, 128] * 2)
+    er = _strides([32 * 64 * 64, 64 * 64, 64])
+    # the KeyFormer passes take 16-bit inputs only (fp32 attention has its own forward and column kernels)
+    assert lib.dgg_attn_kf_rowlse(FAKE, FAKE, FAKE, er, FAKE, 1, 64, 64, 2, 2, 128, s, 0.1, 1.5, 0, 1, _lib.DGG_F32,
+                                  None) == E_DTYPE
+    assert lib.dgg_attn_kf_colsum(FAKE, FAKE, FAKE, er, FAKE, FAKE, 1, 64, 64, 2, 2, 128, s, 0.1, 1.5, 0, 1,
+                                  _lib.DGG_F32, None) == E_DTYPE
+    assert lib.dgg_attn_kf_rowlse(FAKE, FAKE, FAKE, er, FAKE, 1, 64, 64, 2, 2, 128, s, 0.1, 0.0, 0, 1, _lib.DGG_F16,
+                                  None) == E_SHAPE  # tau must be > 0
+    assert lib.dgg_attn_kf_rowlse(FAKE, FAKE, None, er, FAKE, 1, 64, 64, 2, 2, 128, s, 0.1, 1.5, 0, 1, _lib.DGG_F16,
+                                  None) == E_NULL
 
 
 def test_decode_validation(lib):
@@ -141,15 +159,11 @@ def test_topk_validation(lib):
     assert lib.dgg_topk_indices(None, 0, 100, 10, None, None) == OK
 
 
-def test_ref_multiplier_validation(lib):
-    y = ctypes.c_float(0.0)
-    assert lib.dgg_ref_multiplier(_lib.DGG_F32, 11.0, ctypes.byref(y)) == E_DTYPE
-    assert lib.dgg_ref_multiplier(_lib.DGG_F16, 11.0, None) == E_NULL
-    # a divisor with an exact reciprocal: the multiplier is found and is that reciprocal
-    assert lib.dgg_ref_multiplier(_lib.DGG_BF16, 4.0, ctypes.byref(y)) == 1
-    assert y.value == 0.25
-    # not finite: no multiplier (the kernels then keep the division sequence)
-    assert lib.dgg_ref_multiplier(_lib.DGG_F16, float("inf"), ctypes.byref(y)) == 0
+def test_clock_probe_validation(lib):
+    assert lib.dgg_clock_probe(None, 100, None) == E_NULL
+    assert lib.dgg_clock_probe(ctypes.c_void_p(0x10004), 100, None) == E_ALIGN
+    assert lib.dgg_clock_probe(FAKE, 0, None) == E_SHAPE
+    assert lib.dgg_clock_probe(FAKE, 2_000_000, None) == E_SHAPE
 
 
 def test_python_wrappers_reject_cpu_tensors():

@@ -85,6 +85,96 @@ def test_prefill_fast_path_matches_oracle(gpu, B, Sq, Sk, Hq, Hkv, causal, windo
     assert_close(got[~nan], ref.float()[~nan], *TOL[torch.bfloat16], what)
 
 
+FP16_NOLSE_CASES = [
+    # fp16 without lse: the v_dot2 row-sum instantiation that compile(Attn / Gemma2) runs for the reference's
+    # default fp16 inputs. B, Sq, Sk, Hq, Hkv, D, causal, softcap, window
+    (1, 512, 512, 2, 2, 128, True, 0.0, 0),
+    (2, 300, 300, 4, 2, 128, True, 0.0, 0),      # ragged, GQA
+    (1, 130, 700, 2, 2, 128, True, 0.0, 0),      # Sq < Sk
+    (1, 700, 130, 2, 2, 128, True, 0.0, 0),      # Sq > Sk: NaN rows
+    (1, 384, 384, 2, 2, 128, True, 50.0, 0),     # soft-cap
+    (1, 333, 333, 2, 2, 128, True, 30.0, 100),   # soft-cap + window
+    (1, 256, 256, 2, 2, 256, True, 0.0, 0),      # head_dim 256
+    (1, 333, 517, 4, 2, 256, True, 0.0, 128),    # head_dim 256, window, GQA, Sq < Sk
+    (1, 200, 200, 2, 2, 256, True, 50.0, 64),    # head_dim 256, soft-cap + window
+    (1, 257, 383, 2, 2, 128, False, 0.0, 0),     # non-causal, ragged key tile
+]
+
+
+@pytest.mark.parametrize("B,Sq,Sk,Hq,Hkv,D,causal,softcap,window", FP16_NOLSE_CASES)
+def test_prefill_fp16_no_lse_matches_oracle(gpu, B, Sq, Sk, Hq, Hkv, D, causal, softcap, window):
+    q, k, v = _qkv(B, Sq, Sk, Hq, Hkv, D, torch.float16, seed=Sq * 5 + Sk + D + 3)
+    ref = oa.attention(q, k, v, causal=causal, softcap=softcap or None, window=window or None)
+    out = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), causal=causal, softcap=softcap, window=window)
+    what = f"fp16 no-lse B{B} Sq{Sq} Sk{Sk} H{Hq}/{Hkv} D{D} causal={causal} cap={softcap} win={window}"
+    got, want = out.cpu().float(), ref.float()
+    nan = torch.isnan(want)
+    assert torch.equal(torch.isnan(got), nan), what + " NaN rows"
+    assert_close(got[~nan], want[~nan], *TOL[torch.float16], what)
+
+
+F32_CASES = [
+    # B, Sq, Sk, Hq, Hkv, D, causal, softcap, window
+    (1, 512, 512, 8, 8, 64, True, 0.0, 0),       # config 1's shape
+    (2, 200, 300, 4, 2, 128, True, 0.0, 0),      # GQA, Sq < Sk
+    (1, 300, 130, 2, 2, 64, True, 0.0, 0),       # Sq > Sk: NaN rows, lse -inf
+    (1, 192, 192, 2, 1, 256, True, 50.0, 64),    # soft-cap + window, head_dim 256
+    (1, 100, 170, 2, 2, 128, False, 0.0, 0),     # non-causal
+]
+
+
+@pytest.mark.parametrize("B,Sq,Sk,Hq,Hkv,D,causal,softcap,window", F32_CASES)
+def test_prefill_fp32_matches_oracle(gpu, B, Sq, Sk, Hq, Hkv, D, causal, softcap, window):
+    q, k, v = _qkv(B, Sq, Sk, Hq, Hkv, D, torch.float32, seed=Sq + Sk + D + 9)
+    ref, ref_lse = oa.attention(q, k, v, causal=causal, softcap=softcap or None, window=window or None,
+                                return_lse=True)
+    out, lse = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), causal=causal, softcap=softcap, window=window,
+                           return_lse=True)
+    what = f"fp32 B{B} Sq{Sq} Sk{Sk} H{Hq}/{Hkv} D{D} causal={causal} cap={softcap} win={window}"
+    assert out.dtype == torch.float32
+    assert_close(out.cpu(), ref, 1e-5, 1e-5, what + " out")
+    fin = torch.isfinite(ref_lse)
+    assert torch.equal(torch.isfinite(lse.cpu()), fin), what + " lse -inf pattern"
+    assert_close(lse.cpu()[fin], ref_lse[fin], 1e-5, 1e-6, what + " lse")
+
+
+def test_config1_fp32_on_gpu(gpu):
+    # config 1 (fp32, B=1, H=8, S=512, D=64) through the C ABI: O and LSE against the oracle, and through the
+    # drop-in compile(Attn) callable
+    from deepgengraph_amd import configs as C
+
+    cfg = C.CFG1
+    q, k, v, _ = C.attn_inputs(cfg)
+    ref, ref_lse = oa.attention(q, k, v, causal=True, return_lse=True)
+    out, lse = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), causal=True, return_lse=True)
+    assert_close(out.cpu(), ref, 1e-5, 1e-5, "config 1 O")
+    assert_close(lse.cpu(), ref_lse, 1e-5, 1e-6, "config 1 LSE")
+    model = ocases.Attn(kv_head_num=8, head_num=8, head_dim=64)
+    f = dgg_compile(model=model, input_names=["q", "k", "v"], inputs=[q, k, v], output_names=["out"],
+                    system="mi355x")
+    assert_close(f(q.to(gpu), k.to(gpu), v.to(gpu)).cpu(), ref, 1e-5, 1e-5, "config 1 via compile(Attn)")
+
+
+def test_fp32_column_scores_match_oracle(gpu):
+    # fp32 H2O / RoCo / Corm column passes (no 16-bit rounding point: reference rounding changes nothing)
+    S, H, D = 300, 2, 64
+    g = torch.Generator().manual_seed(21)
+    q, k, v = (torch.randn(1, S, H, D, generator=g) for _ in range(3))
+    k[:, torch.randperm(S, generator=g)[:5]] *= 4.0
+    ref_out, ref_cs, _ = oa.h2o(q, k, v)
+    out, cs = A.h2o_attention(q.to(gpu), k.to(gpu), v.to(gpu))
+    assert_close(out.cpu(), ref_out, 1e-5, 1e-5, "fp32 h2o out")
+    _colsum_check(cs.cpu(), ref_cs, "fp32 h2o colsum")
+    _, s1, s2, _ = oa.roco(q, k, v)
+    _, g1, g2 = A.roco_attention(q.to(gpu), k.to(gpu), v.to(gpu))
+    _colsum_check(g1.cpu(), s1, "fp32 roco sum")
+    _colsum_check(g2.cpu(), s2, "fp32 roco sum of squares")
+    thr = oa.corm_mask(S, S)
+    _, hit, _ = oa.corm(q, k, v, thr)
+    _, ghit = A.corm_attention(q.to(gpu), k.to(gpu), v.to(gpu), thr.to(gpu))
+    assert torch.equal(ghit.cpu(), hit)
+
+
 @pytest.mark.parametrize("name,kw,dtype", [
     ("attn_d64_causal_bf16", dict(causal=True), torch.bfloat16),
     ("attn_d64_gqa_softcap_window_bf16", dict(causal=True, softcap=5.0, window=33), torch.bfloat16),
@@ -206,25 +296,90 @@ def test_topk_kernel_golden_and_ties(gpu):
         np.testing.assert_array_equal(got, osel.topk_indices(vals, k), err_msg=f"n={n} k={k}")
 
 
-@pytest.mark.parametrize("case_cls,kw,dtype", [
-    (ocases.Attn, dict(kv_head_num=4, head_num=4, head_dim=128), torch.bfloat16),
-    (ocases.Gemma2, dict(kv_head_num=4, head_num=4, head_dim=128), torch.bfloat16),
-    (ocases.H2O, dict(kv_head_num=4, head_num=4, head_dim=128), torch.float16),
+@pytest.mark.parametrize("case_cls,kw,dtype,q_len,kv_len", [
+    (ocases.Attn, dict(kv_head_num=4, head_num=4, head_dim=128), torch.bfloat16, 384, 384),
+    (ocases.Gemma2, dict(kv_head_num=4, head_num=4, head_dim=128), torch.bfloat16, 384, 384),
+    (ocases.H2O, dict(kv_head_num=4, head_num=4, head_dim=128), torch.float16, 384, 384),
+    # the reference's default dtype (fp16, attn.py:36 / gemma2.py:41), ragged and unequal lengths
+    (ocases.Attn, dict(kv_head_num=4, head_num=4, head_dim=128), torch.float16, 384, 384),
+    (ocases.Attn, dict(kv_head_num=4, head_num=4, head_dim=128), torch.float16, 333, 517),
+    (ocases.Gemma2, dict(kv_head_num=4, head_num=4, head_dim=128), torch.float16, 384, 384),
+    (ocases.Gemma2, dict(kv_head_num=2, head_num=2, head_dim=256), torch.float16, 300, 300),
+    (ocases.Gemma2, dict(kv_head_num=4, head_num=4, head_dim=128), torch.float16, 517, 333),
+    # fp32 (config 1's dtype) and decode-shaped calls (q_len == 1: attn.py:22-23 masks nothing)
+    (ocases.Attn, dict(kv_head_num=8, head_num=8, head_dim=64), torch.float32, 256, 256),
+    (ocases.Attn, dict(kv_head_num=8, head_num=8, head_dim=128), torch.float16, 1, 4096),
+    (ocases.Attn, dict(kv_head_num=4, head_num=4, head_dim=64), torch.bfloat16, 1, 1000),
+    (ocases.Attn, dict(kv_head_num=4, head_num=4, head_dim=256), torch.float16, 1, 777),
 ])
-def test_compile_drop_in(gpu, case_cls, kw, dtype):
+def test_compile_drop_in(gpu, case_cls, kw, dtype, q_len, kv_len):
     # run_kernel.py:44-78 flow: build the case, prepare inputs, compile with the MI355X system, compare outputs
     model = case_cls(**kw).eval()
-    specs = model.prepare(q_len=384, kv_len=384, dtype=dtype, seed=3)
+    specs = model.prepare(batch_size=2 if q_len == 1 else 1, q_len=q_len, kv_len=kv_len, dtype=dtype, seed=3)
     names = list(specs["input"].keys())
     inputs = [specs["input"][n] for n in names]
     f = dgg_compile(model=model, input_names=names, inputs=inputs, output_names=specs["output"], system="mi355x")
     outs = f(*[t.to(gpu) for t in inputs])
     refs = model(*inputs)
+    tol = TOL.get(dtype, (1e-5, 1e-5))
+    what = f"{case_cls.__name__} {dtype} q_len={q_len} kv_len={kv_len}"
     if isinstance(refs, tuple):
         assert isinstance(outs, tuple) and len(outs) == len(refs)
-        assert_close(outs[0].cpu().float(), refs[0].float(), *TOL[dtype], "h2o out")
-        _colsum_check(outs[1].cpu(), refs[1], "h2o score")
+        assert_close(outs[0].cpu().float(), refs[0].float(), *tol, what + " out")
+        _colsum_check(outs[1].cpu(), refs[1], what + " score")
         assert outs[1].shape == refs[1].shape
     else:
         assert outs.shape == refs.shape and outs.dtype == refs.dtype
-        assert_close(outs.cpu().float(), refs.float(), *TOL[dtype], case_cls.__name__)
+        got, want = outs.cpu().float(), refs.float()
+        nan = torch.isnan(want)
+        assert torch.equal(torch.isnan(got), nan), what + " NaN rows"
+        assert_close(got[~nan], want[~nan], *tol, what)
+
+
+@pytest.mark.parametrize("B,H,Hkv,L,D,dtype", [
+    (4, 8, 8, 4096, 128, torch.float16),
+    (3, 8, 2, 3000, 64, torch.bfloat16),    # GQA, ragged split
+    (2, 4, 4, 300, 256, torch.float16),
+])
+def test_decode_shaped_prefill_call_matches_oracle(gpu, B, H, Hkv, L, D, dtype):
+    # attention() with one query row runs on the split-KV decode kernels, reading the case layout [B, L, H, D]
+    # through its strides; output and lse (both bases) against the oracle
+    q, k, v = _qkv(B, 1, L, H, Hkv, D, dtype, seed=L + D)
+    ref, ref_lse = oa.attention(q, k, v, causal=True, return_lse=True)
+    out, lse = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), causal=True, return_lse=True)
+    what = f"decode-shaped B{B} H{H}/{Hkv} L{L} D{D} {dtype}"
+    assert_close(out.cpu().float(), ref.float(), *TOL[dtype], what + " out")
+    assert_close(lse.cpu(), ref_lse, 1e-3, 1e-4, what + " lse")
+    _, lse2 = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), causal=True, return_lse=True, lse_base2=True)
+    assert_close(lse2.cpu(), ref_lse * math.log2(math.e), 1e-3, 1e-4, what + " lse base 2")
+
+
+def test_h2o_matches_torch_eager_on_gpu(gpu):
+    """H2O with reference rounding against the reference formula run by torch itself on the GPU (the case module
+    of the 'torch' system, h2o.py:18-38, on the same fp16 inputs with x4 sink keys): the scores go through torch's
+    own GPU matmul rounding and GPU division by sqrt(D). Column sums within 1e-3 and identical top-256 sets; the
+    score gap at the selection boundary is reported on failure."""
+    from deepgengraph_amd import cases as tcases
+
+    S, H, D, kk = 2048, 8, 128, 256
+    g = torch.Generator().manual_seed(4242)
+    q = torch.randn(1, S, H, D, generator=g)
+    k = torch.randn(1, S, H, D, generator=g)
+    v = torch.randn(1, S, H, D, generator=g)
+    k[:, torch.randperm(S, generator=g)[:16]] *= 4.0
+    q, k, v = (t.half().to(gpu) for t in (q, k, v))
+    prev = torch.backends.cuda.matmul.allow_fp16_reduced_precision_reduction
+    torch.backends.cuda.matmul.allow_fp16_reduced_precision_reduction = False  # fp32 accumulation, one rounding
+    try:
+        ref_out, ref_cs = tcases.H2O(kv_head_num=H, head_num=H, head_dim=D)(q, k, v)
+    finally:
+        torch.backends.cuda.matmul.allow_fp16_reduced_precision_reduction = prev
+    out, cs = A.h2o_attention(q, k, v)
+    assert_close(out.cpu().float(), ref_out.cpu().float(), *TOL[torch.float16], "h2o out vs torch on GPU")
+    _colsum_check(cs.cpu(), ref_cs.cpu(), "h2o score vs torch on GPU")
+    got = A.topk_indices(cs, kk).cpu().numpy()
+    want = osel.topk_indices(ref_cs.cpu().numpy(), kk)
+    if not np.array_equal(got, want):
+        srt = np.sort(ref_cs.cpu().numpy(), axis=-1)[..., ::-1]
+        gap = srt[..., kk - 1] - srt[..., kk]
+        raise AssertionError(f"top-{kk} sets differ; reference score gap at rank {kk}: min {gap.min():.3e}")

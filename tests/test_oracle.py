@@ -88,15 +88,97 @@ def test_attention_reductions():
     assert_close(oa.attention(q, k, v, window=1), v.repeat_interleave(2, dim=2), 1e-6, 1e-6, "window 1")
 
 
-def test_attention_low_precision_rounding_points():
-    # bf16 oracle stays within the bf16 tolerance of the fp32 evaluation of the same (exactly representable) inputs
+def test_attention_low_precision_within_tolerance_of_fp32():
+    # the bf16 oracle stays within the bf16 tolerance of the fp32 evaluation of the same (exactly representable)
+    # inputs; the individual rounding points are pinned step by step in test_ref_rounding.py
     torch.manual_seed(2)
     q, k, v = (torch.randn(1, 64, 2, 64).bfloat16() for _ in range(3))
     lo = oa.attention(q, k, v)
     hi = oa.attention(q.float(), k.float(), v.float())
     assert lo.dtype == torch.bfloat16
     assert_close(lo.float(), hi, 2e-2, 1e-2, "bf16 vs fp32")
-    assert not torch.equal(lo.float(), hi.bfloat16().float()), "scores must be rounded to bf16 before the softmax"
+
+
+def test_config1_at_size_against_float64():
+    """Config 1 (fp32 causal MHA, B=1, H=8, S=512, D=64, N(0,1) inputs, scale 1/8) at its full size: the oracle's
+    O [B, S, H, D] and natural-log LSE [B, H, S] against a float64 numpy evaluation of the same formula."""
+    from deepgengraph_amd import configs as C
+
+    cfg = C.CFG1
+    q, k, v, _ = C.attn_inputs(cfg)
+    assert q.dtype == torch.float32 and tuple(q.shape) == (1, 512, 8, 64)
+    out, lse = oa.attention(q, k, v, causal=True, return_lse=True)
+    qn, kn, vn = (t.double().numpy().transpose(0, 2, 1, 3) for t in (q, k, v))  # [B, H, S, D]
+    s = qn @ kn.transpose(0, 1, 3, 2) / 8.0
+    s = np.where(np.triu(np.ones((512, 512), bool), 1), -np.inf, s)
+    m = s.max(-1, keepdims=True)
+    e = np.exp(s - m)
+    ref_lse = (m[..., 0] + np.log(e.sum(-1)))
+    ref_out = ((e / e.sum(-1, keepdims=True)) @ vn).transpose(0, 2, 1, 3)
+    assert_close(out, ref_out, 1e-5, 1e-5, "config 1 O")
+    assert_close(lse, ref_lse, 1e-5, 1e-6, "config 1 LSE")
+
+
+def _block_float64(x, w_norm, w_qkv, w_o, heads, kv_heads, eps, theta, *, rotate_v=False, split=("q", "k", "v"),
+                   k_pos_offset=0):
+    """models/attn.py:34-53 + LlamaLayer's norm (models/attn.py:71-74) composed from the float64 brute-force
+    pieces, with both projections as explicit loops (y = x W^T, W stored [out, in]). The keyword arguments plant
+    the mistakes the oracle must not make (rotating v, another split order, k rotated at shifted positions)."""
+    S, hidden = len(x), len(x[0])
+    D = hidden // heads
+    h = brute.rms_norm(x, w_norm, eps)
+    n_out = len(w_qkv)
+    qkv = [[sum(h[t][i] * float(w_qkv[o][i]) for i in range(hidden)) for o in range(n_out)] for t in range(S)]
+    sizes = {"q": heads * D, "k": kv_heads * D, "v": kv_heads * D}
+    parts, c = {}, 0
+    for name in split:
+        parts[name] = [row[c:c + sizes[name]] for row in qkv]
+        c += sizes[name]
+    pos = list(range(S))
+    q = brute.rotary(pos, parts["q"], D, theta)
+    k = brute.rotary([t + k_pos_offset for t in pos], parts["k"], D, theta)
+    v = brute.rotary(pos, parts["v"], D, theta) if rotate_v else parts["v"]
+    q4 = [[[q[t][hh * D:(hh + 1) * D] for hh in range(heads)] for t in range(S)]]
+    k4 = [[[k[t][hh * D:(hh + 1) * D] for hh in range(kv_heads)] for t in range(S)]]
+    v4 = [[[v[t][hh * D:(hh + 1) * D] for hh in range(kv_heads)] for t in range(S)]]
+    o, _ = brute.attention(q4, k4, v4, causal=True)
+    of = [[o[0][t][hh][d] for hh in range(heads) for d in range(D)] for t in range(S)]
+    return [[sum(of[t][i] * float(w_o[r][i]) for i in range(hidden)) for r in range(hidden)] for t in range(S)]
+
+
+def test_attention_block_against_float64_composition():
+    """oracle.llama.attention_block (config 2's block) on a tiny GQA block (hidden 64, 4 heads, 2 KV heads, S=16)
+    against the float64 composition of brute.rms_norm, brute.rotary, brute.attention and loop projections. Each
+    planted mistake of the composition (v rotated, W used untransposed, q/k split swapped, k rotated one position
+    off q) must move the result far outside the tolerance, so the comparison can see it. (Shifting q and k by the
+    same offset is invisible by construction: rotary scores depend only on the position difference, which
+    test_rotary checks.)"""
+    from oracle import llama as ol
+
+    g = torch.Generator().manual_seed(11)
+    S, hidden, heads, kv_heads = 16, 64, 4, 2
+    D = hidden // heads
+    x = torch.randn(1, S, hidden, generator=g)
+    w_norm = 1 + 0.02 * torch.randn(hidden, generator=g)
+    w_qkv = 0.2 * torch.randn((heads + 2 * kv_heads) * D, hidden, generator=g)
+    w_o = 0.2 * torch.randn(hidden, hidden, generator=g)
+    eps, theta = 1e-6, 100.0  # a small theta turns every rotary pair at these positions
+    out = ol.attention_block(x, w_norm, w_qkv, w_o, heads=heads, kv_heads=kv_heads, eps=eps, theta=theta)
+    args = (x[0].tolist(), w_norm.tolist(), w_qkv.tolist(), w_o.tolist(), heads, kv_heads, eps, theta)
+    ref = torch.tensor(_block_float64(*args), dtype=torch.float64)
+    assert_close(out[0], ref, 1e-4, 1e-4, "attention block")
+    planted = {
+        "v rotated": _block_float64(*args, rotate_v=True),
+        "k/q split swapped": _block_float64(*args, split=("k", "q", "v")),
+        "k positions off by one": _block_float64(*args, k_pos_offset=1),
+    }
+    # W used untransposed: only shapes where it multiplies at all, i.e. the square output projection
+    wt = w_o.t().contiguous()
+    planted["W_o untransposed"] = _block_float64(x[0].tolist(), w_norm.tolist(), w_qkv.tolist(), wt.tolist(), heads,
+                                                 kv_heads, eps, theta)
+    for what, bad in planted.items():
+        err = (torch.tensor(bad, dtype=torch.float64) - ref).abs().max().item()
+        assert err > 1e-2, f"planted mistake '{what}' is not visible ({err:.2e})"
 
 
 def test_decode_matches_attention_and_splitkv():

@@ -54,6 +54,8 @@ SIGNATURES = {
     "dgg_nonzero_workspace_bytes": (_i64, [_i64]),
     "dgg_nonzero": (_i32, [_vp, _i32, _i64p, _vp, _i64, _vp, _vp, _i64, _vp]),
     "dgg_clock_probe": (_i32, [_vp, _i64, _vp]),
+    "dgg_attn_decode_noalloc": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64p, _i64, _f32, _i32,
+                                       _vp]),
     "dgg_attn_decode_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "dgg_attn_decode": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64p, _i64, _f32,
                                _i32, _vp]),

@@ -8,6 +8,7 @@
 // merged once through LDS into the split's partial (unnormalised output, max, sum) in the workspace.
 // A second small kernel merges the splits of each (batch, head).
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 
@@ -284,10 +285,54 @@ extern "C" int64_t dgg_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_
   return B * Hq * splits * (D + 2) * (int64_t)sizeof(float);
 }
 
-extern "C" int dgg_attn_decode(const void* q, const void* k, const void* v, void* o, float* lse, void* workspace,
-                               int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
-                               const int64_t* strides, int64_t splits, float scale, int dtype, void* stream) {
-  const char* op = "attn_decode";
+namespace {
+
+// ------------------------------------------------------------------------------------------------
+// Allocation-free decode. The split partials live in `scratch`, a file-scope device array of
+// kDecodeScratchBytes that every GPU the library runs on holds until the process ends. Host code never passes
+// the array's name to a kernel (on the host it is only a stand-in for the symbol): the device address is looked
+// up once per device with hipGetSymbolAddress and cached. The partial kernel writes every (batch, head, split)
+// entry before the merge reads it, so nothing needs clearing between calls; calls that overlap on one GPU share
+// the array and race.
+// ------------------------------------------------------------------------------------------------
+constexpr int64_t kDecodeScratchBytes = 96ll << 20;
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this device's `scratch`, for the device the stream runs on (which must be current).
+int device_scratch(const char* op, void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  DGG_REQUIRE(e == hipSuccess, DGG_ERR_LAUNCH, "%s: hipGetDevice failed: %s", op, hipGetErrorString(e));
+  DGG_REQUIRE(dev >= 0 && dev < kMaxDevices, DGG_ERR_LAUNCH, "%s: device %d out of range", op, dev);
+  if (stream != nullptr) {
+    int sdev = -1;
+    e = hipStreamGetDevice(dgg::as_stream(stream), &sdev);
+    DGG_REQUIRE(e == hipSuccess, DGG_ERR_LAUNCH, "%s: hipStreamGetDevice failed: %s", op, hipGetErrorString(e));
+    DGG_REQUIRE(sdev == dev, DGG_ERR_LAUNCH, "%s: the stream belongs to device %d but device %d is current", op, sdev,
+                dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    DGG_REQUIRE(e == hipSuccess && ptr != nullptr, DGG_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed: %s", op,
+                hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return DGG_OK;
+}
+
+// Shared body of dgg_attn_decode and dgg_attn_decode_noalloc: validates every argument, then launches the
+// partial and merge kernels with the partials in `workspace` (use_scratch: in this device's `scratch` instead,
+// workspace_bytes being its fixed size).
+int decode_impl(const char* op, const void* q, const void* k, const void* v, void* o, float* lse, void* workspace,
+                int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
+                const int64_t* strides, int64_t splits, float scale, int dtype, void* stream, bool use_scratch) {
   DGG_REQUIRE(dtype == DGG_F16 || dtype == DGG_BF16, DGG_ERR_DTYPE,
               "%s: dtype code %d not supported (attention kernels take f16 or bf16)", op, dtype);
   DGG_REQUIRE(D == 64 || D == 128 || D == 256, DGG_ERR_UNSUPPORTED, "%s: head_dim %lld not supported (64, 128, 256)",
@@ -304,10 +349,19 @@ extern "C" int dgg_attn_decode(const void* q, const void* k, const void* v, void
     DGG_REQUIRE(strides[i] >= 0 && strides[i] % 8 == 0, DGG_ERR_STRIDE,
                 "%s: stride[%d] = %lld must be a non-negative multiple of 8 elements", op, i, (long long)strides[i]);
   const int64_t need = dgg_attn_decode_workspace_bytes(B, Hq, D, splits);
-  DGG_REQUIRE(workspace_bytes >= need, DGG_ERR_WORKSPACE, "%s: workspace of %lld bytes < required %lld", op,
-              (long long)workspace_bytes, (long long)need);
+  if (use_scratch)
+    DGG_REQUIRE(need <= workspace_bytes, DGG_ERR_WORKSPACE,
+                "%s: the split partials need %lld bytes, more than the fixed scratch of %lld bytes (use fewer splits, "
+                "or dgg_attn_decode with a workspace)", op, (long long)need, (long long)workspace_bytes);
+  else
+    DGG_REQUIRE(workspace_bytes >= need, DGG_ERR_WORKSPACE, "%s: workspace of %lld bytes < required %lld", op,
+                (long long)workspace_bytes, (long long)need);
   if (B == 0) return DGG_OK;
-  DGG_REQUIRE(q && k && v && o && workspace, DGG_ERR_NULL, "%s: null pointer", op);
+  DGG_REQUIRE(q && k && v && o, DGG_ERR_NULL, "%s: null pointer", op);
+  if (use_scratch) {
+    if (int rc = device_scratch(op, stream, &workspace)) return rc;
+  }
+  DGG_REQUIRE(workspace != nullptr, DGG_ERR_NULL, "%s: null workspace", op);
   DGG_REQUIRE(dgg::aligned16(q) && dgg::aligned16(k) && dgg::aligned16(v) && dgg::aligned16(workspace),
               DGG_ERR_ALIGN, "%s: q/k/v/workspace must be 16-byte aligned", op);
   DecodeParams p{};
@@ -341,6 +395,22 @@ extern "C" int dgg_attn_decode(const void* q, const void* k, const void* v, void
     else launch_decode<F16, 256>(p, st);
   }
   return dgg::check_launch(op);
+}
+
+}  // namespace
+
+extern "C" int dgg_attn_decode(const void* q, const void* k, const void* v, void* o, float* lse, void* workspace,
+                               int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
+                               const int64_t* strides, int64_t splits, float scale, int dtype, void* stream) {
+  return decode_impl("attn_decode", q, k, v, o, lse, workspace, workspace_bytes, B, Hq, Hkv, L, D, strides, splits,
+                     scale, dtype, stream, false);
+}
+
+extern "C" int dgg_attn_decode_noalloc(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B,
+                                       int64_t Hq, int64_t Hkv, int64_t L, int64_t D, const int64_t* strides,
+                                       int64_t splits, float scale, int dtype, void* stream) {
+  return decode_impl("attn_decode_noalloc", q, k, v, o, lse, nullptr, kDecodeScratchBytes, B, Hq, Hkv, L, D, strides,
+                     splits, scale, dtype, stream, true);
 }
 
 extern "C" int dgg_topk_indices(const float* scores, int64_t rows, int64_t n, int64_t k, int64_t* out_idx,

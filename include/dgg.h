@@ -188,6 +188,16 @@ int64_t dgg_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_
 int dgg_attn_decode(const void* q, const void* k, const void* v, void* o, float* lse, void* workspace,
                     int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
                     const int64_t* strides, int64_t splits, float scale, int dtype, void* stream);
+/* dgg_attn_decode without a workspace argument, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc); no counterpart in the reference. The split
+ * partials live in a fixed 96 MiB (100663296-byte) device array that each GPU the library runs on holds until the
+ * process ends; a call whose partials, B * Hq * splits * (D + 2) * 4 bytes, exceed it returns
+ * DGG_ERR_WORKSPACE. Nothing is allocated and nothing needs clearing between calls, but every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams, other threads) race. The stream must
+ * belong to the current device. Arguments otherwise as dgg_attn_decode, with the same results. */
+int dgg_attn_decode_noalloc(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t Hq,
+                            int64_t Hkv, int64_t L, int64_t D, const int64_t* strides, int64_t splits, float scale,
+                            int dtype, void* stream);
 
 /* Shader-clock probe (no counterpart in the reference: measurement support for the benchmark). One lane spins for
  * `ticks` ticks of the constant 100 MHz real-time counter and writes out[0] = shader cycles elapsed (s_memtime),

@@ -159,6 +159,28 @@ def test_topk_validation(lib):
     assert lib.dgg_topk_indices(None, 0, 100, 10, None, None) == OK
 
 
+def test_decode_noalloc_validation(lib):
+    # every argument is checked before the device's scratch is looked up (no GPU needed for these)
+    s = _strides([32 * 128, 128, 32 * 4096 * 128, 4096 * 128, 128] + [32 * 4096 * 128, 4096 * 128, 128] + [32 * 128, 128])
+
+    def call(**kw):
+        a = dict(q=FAKE, k=FAKE, v=FAKE, o=FAKE, lse=None, B=2, Hq=32, Hkv=32, L=4096, D=128, strides=s, splits=8,
+                 scale=0.088, dtype=_lib.DGG_F16)
+        a.update(kw)
+        return lib.dgg_attn_decode_noalloc(a["q"], a["k"], a["v"], a["o"], a["lse"], a["B"], a["Hq"], a["Hkv"], a["L"],
+                                           a["D"], a["strides"], a["splits"], ctypes.c_float(a["scale"]), a["dtype"],
+                                           None)
+
+    assert call(dtype=_lib.DGG_F32) == E_DTYPE
+    assert call(D=96) == E_UNSUP
+    assert call(splits=0) == E_SHAPE
+    assert call(strides=None) == E_NULL
+    assert call(B=128, splits=64) == E_WS  # 136 MB of partials > the 96 MiB scratch
+    assert b"fixed scratch" in lib.dgg_last_error()
+    assert call(q=None) == E_NULL
+    assert call(B=0) == OK
+
+
 def test_clock_probe_validation(lib):
     assert lib.dgg_clock_probe(None, 100, None) == E_NULL
     assert lib.dgg_clock_probe(ctypes.c_void_p(0x10004), 100, None) == E_ALIGN

@@ -256,10 +256,16 @@ def bench_block(args, dev):
     from deepgengraph_amd.llama import LlamaAttentionBlock
 
     inp = C.llama_block_inputs(device=dev)
-    blk = LlamaAttentionBlock(inp["w_norm"], inp["w_qkv"], inp["w_o"], heads=32, kv_heads=32, eps=C.LLAMA_EPS,
-                              rope_theta=C.LLAMA_THETA)
-    ms = _events_time(lambda: blk(inp["x"]), 10, 2)
-    return dict(ms=round(ms, 4))
+    # query rotary inside the attention kernel (the default) or the rotary kernel on q and k: timed in alternation
+    # (medians of 6 runs each) so that clock drift does not favour either
+    blks = {fuse: LlamaAttentionBlock(inp["w_norm"], inp["w_qkv"], inp["w_o"], heads=32, kv_heads=32,
+                                      eps=C.LLAMA_EPS, rope_theta=C.LLAMA_THETA, fuse_rope=fuse)
+            for fuse in (True, False)}
+    times = {True: [], False: []}
+    for i in range(6):
+        for fuse in ((True, False) if i % 2 == 0 else (False, True)):
+            times[fuse].append(_events_time(lambda: blks[fuse](inp["x"]), 10, 2))
+    return dict(ms=round(statistics.median(times[True]), 4), unfused_rope_ms=round(statistics.median(times[False]), 4))
 
 
 def bench_copycal(args, dev):
@@ -340,7 +346,9 @@ def main():
     if "variants" in sections:
         extra["variants"] = bench_variants(args, dev)
     if "block" in sections:
-        extra["cfg2_block_ms"] = bench_block(args, dev)["ms"]
+        blk = bench_block(args, dev)
+        extra["cfg2_block_ms"] = blk["ms"]
+        extra["cfg2_block_unfused_rope_ms"] = blk["unfused_rope_ms"]
     if "copycal" in sections:
         extra["copy_calibration"] = bench_copycal(args, dev)
     line = {

@@ -50,9 +50,23 @@ def decode_splits(B: int, Hq: int, L: int) -> int:
     return int(max(1, min(1024, want, -(-L // 128))))
 
 
+def rotary_cos_sin(positions: torch.Tensor, head_dim: int, rope_theta: float) -> torch.Tensor:
+    """The (cos, sin) table of rotary_embedding_online (csrc/pos_encoding.cu:83-86) for the positions: fp32
+    [n, head_dim], row t = cos of the head_dim/2 angles pos[t] / theta^(2i/head_dim), then their sines. Feeds the
+    query rotation fused into attention(..., rope_cos_sin=...)."""
+    dev = _lib.require_gpu(positions)
+    if positions.dtype != torch.int32 or not positions.is_contiguous():
+        raise RuntimeError("rotary_cos_sin: positions must be a contiguous int32 tensor")
+    n = positions.numel()
+    out = torch.empty(n, head_dim, dtype=torch.float32, device=positions.device)
+    _lib.call("dgg_rotary_cos_sin", _lib.ptr(positions), _lib.ptr(out), n, int(head_dim), float(rope_theta),
+              _lib.stream_handle(dev))
+    return out
+
+
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool = True, softcap: float = 0.0,
               window: int = 0, scale: float | None = None, return_lse: bool = False, ref_rounding: bool = False,
-              out: torch.Tensor | None = None, lse_base2: bool = False):
+              out: torch.Tensor | None = None, lse_base2: bool = False, rope_cos_sin: torch.Tensor | None = None):
     """Fused attention forward. q [B, Sq, Hq, D]; k, v [B, Sk, Hkv, D]; returns out [B, Sq, Hq, D] (q.dtype)
     and, with return_lse, lse [B, Hq, Sq] fp32 (natural log; base 2 with lse_base2, the form
     attention_colsum(..., lse_base2=True) reads fastest).
@@ -62,8 +76,12 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool
     bottom-right aligned causal mask (attn.py:22-23), optional sliding window (key j visible iff
     i + Sk - Sq - j < window), fp32 softmax, P.V. ref_rounding rounds the scores to the input dtype at the
     reference's rounding points (slower; used for H2O selection parity). A one-row call over at least
-    DECODE_MIN_KEYS keys (the reference's decode case) runs on the split-KV decode kernels."""
-    dev = _lib.require_gpu(q, k, v, out)
+    DECODE_MIN_KEYS keys (the reference's decode case) runs on the split-KV decode kernels.
+
+    rope_cos_sin (head_dim 128, 16-bit inputs): q is taken unrotated and each query row is rotated inside the
+    kernel by its row of this table (rotary_cos_sin of the rows' positions, [B * Sq, 128], batch-major), as
+    rotary_embedding_online would have rotated it in place (models/attn.py:41); q is not modified."""
+    dev = _lib.require_gpu(q, k, v, out, rope_cos_sin)
     for name, t in (("q", q), ("k", k), ("v", v)):
         _check_bshd(name, t)
     B, Sq, Hq, D = q.shape
@@ -80,6 +98,17 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool
             raise RuntimeError("attention: out must match q in shape and dtype")
     lse = torch.empty(B, Hq, Sq, dtype=torch.float32, device=q.device) if return_lse else None
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    if rope_cos_sin is not None:
+        if (rope_cos_sin.dtype != torch.float32 or not rope_cos_sin.is_contiguous()
+                or tuple(rope_cos_sin.shape) != (B * Sq, D)):
+            raise RuntimeError(f"attention: rope_cos_sin must be a contiguous fp32 [{B * Sq}, {D}] tensor")
+        flags = ((_lib.ATTN_CAUSAL if causal else 0) | (_lib.ATTN_REF_ROUNDING if ref_rounding else 0)
+                 | (_lib.ATTN_LSE_BASE2 if lse_base2 else 0))
+        strides = _lib.int64_array([*q.stride()[:3], *k.stride()[:3], *v.stride()[:3], *out.stride()[:3]])
+        _lib.call("dgg_attn_prefill_rope", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out), _lib.ptr(lse), B, Sq,
+                  Sk, Hq, Hkv, D, strides, scale, float(softcap or 0.0), int(window or 0), flags,
+                  _lib.dtype_code(q.dtype), _lib.ptr(rope_cos_sin), _lib.stream_handle(dev))
+        return (out, lse) if return_lse else out
     if _decode_shaped(Sq, Sk, softcap, window, ref_rounding, q.dtype):
         # One query row (attn.py:22-23: the bottom-right causal mask hides nothing): the split-KV decode kernels,
         # reading the case layout [B, L, H, D] through its strides.

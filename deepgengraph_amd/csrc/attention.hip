@@ -492,6 +492,25 @@ attn_fwd_dma_kernel(AttnParams p) {
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) qf[n][kk] = ld16<V8>(qp + (int64_t)qi * p.q_ss + 16 * kk + 8 * g);
   }
+  // Fused rotary of the query (head_dim 128): the (cos, sin) of this lane's 32 rotary pairs, loaded with Q so that
+  // the two latencies overlap. The lane holds elements 16kk + 8g + e of fragment kk and their pair partners (+64)
+  // in fragment kk + 4, so it rotates its own pairs.
+  constexpr int NRC = D == 128 ? NQB : 0;
+  f32x8 rcos[NRC > 0 ? NRC : 1][4], rsin[NRC > 0 ? NRC : 1][4];
+  const bool rope = D == 128 && p.rope_cs != nullptr;
+  if constexpr (NRC > 0) {
+    if (rope) {
+#pragma unroll
+      for (int n = 0; n < NQB; ++n) {
+        const float* cs = p.rope_cs + ((int64_t)b * p.Sq + min(qw0 + 32 * n + r, p.Sq - 1)) * D + 8 * g;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          rcos[n][kk] = *reinterpret_cast<const f32x8*>(cs + 16 * kk);
+          rsin[n][kk] = *reinterpret_cast<const f32x8*>(cs + 64 + 16 * kk);
+        }
+      }
+    }
+  }
   // BIAS (bf16 without soft-cap or reference rounding, no lse): Q is pre-scaled by scale*log2(e) and each score
   // accumulator starts from -m (the row's reference maximum) through one extra MFMA whose A fragment is the
   // constant column e_0 and whose B fragment holds -m in k-slot 0. The accumulator then holds s*c - m and
@@ -506,8 +525,28 @@ attn_fwd_dma_kernel(AttnParams p) {
     for (int n = 0; n < NQB; ++n) {
       const bool live = qw0 + 32 * n + r < p.Sq;
 #pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(qf[n][kk]));
+      if constexpr (NRC > 0) {
+        // pos_encoding.cu:90-112 on this lane's row: rotated in fp32, rounded to the storage type as the rotary
+        // kernel stores it
+        if (rope) {
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) {
+            const f32x8 c = rcos[n][kk], sn = rsin[n][kk];
+            const f32x8 x = to_f32x8(qf[n][kk]), y = to_f32x8(qf[n][kk + 4]);
+            f32x8 xo, yo;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              xo[e] = x[e] * c[e] - y[e] * sn[e];
+              yo[e] = y[e] * c[e] + x[e] * sn[e];
+            }
+            qf[n][kk] = from_f32x8<V8>(xo);
+            qf[n][kk + 4] = from_f32x8<V8>(yo);
+          }
+        }
+      }
+#pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) {
-        asm volatile("" : "+v"(qf[n][kk]));
         if (!live) qf[n][kk] = V8{};
         if constexpr (BIAS) qf[n][kk] = from_f32x8<V8>(to_f32x8(qf[n][kk]) * p.c_fast);
         if constexpr (OCC == 1) asm volatile("" : "+a"(qf[n][kk]));
@@ -1443,15 +1482,25 @@ AttnParams make_params(const void* q, const void* k, const void* v, void* o, int
 
 }  // namespace
 
-extern "C" int dgg_attn_prefill(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B,
-                                int64_t Sq, int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides,
-                                float scale, float softcap, int64_t window, uint32_t flags, int dtype, void* stream) {
-  if (int rc = validate_attn("attn_prefill", q, k, B, Sq, Sk, Hq, Hkv, D, strides, 12, scale, softcap, window, dtype))
-    return rc;
+namespace {
+// Shared body of dgg_attn_prefill and dgg_attn_prefill_rope (rope: rotate the query rows by the table rope_cs).
+int prefill_impl(const char* op, const void* q, const void* k, const void* v, void* o, float* lse, int64_t B,
+                 int64_t Sq, int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides, float scale,
+                 float softcap, int64_t window, uint32_t flags, int dtype, bool rope, const float* rope_cs,
+                 void* stream) {
+  if (int rc = validate_attn(op, q, k, B, Sq, Sk, Hq, Hkv, D, strides, 12, scale, softcap, window, dtype)) return rc;
+  if (rope)
+    DGG_REQUIRE(D == 128 && dtype != DGG_F32, DGG_ERR_UNSUPPORTED,
+                "%s: the fused rotary takes head_dim 128 (pos_encoding.cu:195) and 16-bit inputs", op);
   if (B == 0 || Sq == 0) return DGG_OK;
-  DGG_REQUIRE(o && (v || Sk == 0), DGG_ERR_NULL, "attn_prefill: null v/o pointer");
-  DGG_REQUIRE(dgg::aligned16(v) && dgg::aligned16(o), DGG_ERR_ALIGN, "attn_prefill: v/o must be 16-byte aligned");
+  DGG_REQUIRE(o && (v || Sk == 0), DGG_ERR_NULL, "%s: null v/o pointer", op);
+  DGG_REQUIRE(dgg::aligned16(v) && dgg::aligned16(o), DGG_ERR_ALIGN, "%s: v/o must be 16-byte aligned", op);
+  if (rope) {
+    DGG_REQUIRE(rope_cs != nullptr, DGG_ERR_NULL, "%s: null rotary table", op);
+    DGG_REQUIRE(((uintptr_t)rope_cs & 31u) == 0, DGG_ERR_ALIGN, "%s: the rotary table must be 32-byte aligned", op);
+  }
   AttnParams p = make_params(q, k, v, o, B, Sq, Sk, Hq, Hkv, D, scale, softcap, window, flags);
+  p.rope_cs = rope_cs;
   p.lse = lse;
   p.q_sb = strides[0]; p.q_ss = strides[1]; p.q_sh = strides[2];
   p.k_sb = strides[3]; p.k_ss = strides[4]; p.k_sh = strides[5];
@@ -1463,7 +1512,7 @@ extern "C" int dgg_attn_prefill(const void* q, const void* k, const void* v, voi
   if (dtype == DGG_F32) {  // fp32 has no 16-bit rounding point: reference rounding changes nothing
     p.n_tiles = (int)((Sq + f32_rows_per_tile() - 1) / f32_rows_per_tile());
     launch_attn_f32_fwd(p, (int)D, st);
-    return dgg::check_launch("attn_prefill");
+    return dgg::check_launch(op);
   }
   const int64_t bm = D == 128 ? kD128BM : D == 256 ? kD256BM : kBM;
   p.n_tiles = (int)((Sq + bm - 1) / bm);
@@ -1476,7 +1525,23 @@ extern "C" int dgg_attn_prefill(const void* q, const void* k, const void* v, voi
     else if (D == 128) pick_fwd<F16, 128>(p, ref, st);
     else pick_fwd<F16, 256>(p, ref, st);
   }
-  return dgg::check_launch("attn_prefill");
+  return dgg::check_launch(op);
+}
+}  // namespace
+
+extern "C" int dgg_attn_prefill(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B,
+                                int64_t Sq, int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides,
+                                float scale, float softcap, int64_t window, uint32_t flags, int dtype, void* stream) {
+  return prefill_impl("attn_prefill", q, k, v, o, lse, B, Sq, Sk, Hq, Hkv, D, strides, scale, softcap, window, flags,
+                      dtype, false, nullptr, stream);
+}
+
+extern "C" int dgg_attn_prefill_rope(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B,
+                                     int64_t Sq, int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D,
+                                     const int64_t* strides, float scale, float softcap, int64_t window,
+                                     uint32_t flags, int dtype, const float* q_cos_sin, void* stream) {
+  return prefill_impl("attn_prefill_rope", q, k, v, o, lse, B, Sq, Sk, Hq, Hkv, D, strides, scale, softcap, window,
+                      flags, dtype, true, q_cos_sin, stream);
 }
 
 namespace {

@@ -49,6 +49,7 @@ struct AttnParams {
   float softcap;
   float sc_a;    // 2 * scale / softcap * log2(e)
   float sc_b;    // softcap * log2(e)
+  const float* rope_cs;  // fused rotary of the query rows: [B * Sq, D] (cos | sin) per row, or nullptr
 };
 
 // Probability of the perturbed score for KeyFormer: x2 = the score in the exp2 domain, e = exp_rand, l2 = the

@@ -403,6 +403,40 @@ extern "C" int dgg_silu_and_mul(void* out, const void* input, int64_t rows, int6
   }
 }
 
+// (cos, sin) table of the online rotary for the rotation fused into the attention forward: row t holds cos of
+// the D/2 angles pos[t] / theta^(2i/D) followed by their sines, from the same powf / sincosf as
+// rotary_online_kernel (pos_encoding.cu:83-86), so a row rotated through the table is the row the rotary kernel
+// would have written.
+__global__ void __launch_bounds__(256) rotary_cos_sin_kernel(const int32_t* __restrict__ pos, float* __restrict__ cs,
+                                                              int64_t tokens, int D, float theta) {
+  const int half = D / 2;
+  const int64_t n = tokens * half;
+  for (int64_t it = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; it < n; it += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = it / half;
+    const int i = (int)(it - t * half);
+    const float ang = (float)pos[t] / powf(theta, (float)(2 * i) / (float)D);
+    float sn, c;
+    sincosf(ang, &sn, &c);
+    cs[t * D + i] = c;
+    cs[t * D + half + i] = sn;
+  }
+}
+
+extern "C" int dgg_rotary_cos_sin(const int32_t* positions, float* cos_sin, int64_t tokens, int64_t head_dim,
+                                  float rope_theta, void* stream) {
+  DGG_REQUIRE(head_dim > 0 && head_dim % 16 == 0 && head_dim <= 512, DGG_ERR_UNSUPPORTED,
+              "rotary_cos_sin: head_dim must be a positive multiple of 16 up to 512 (got %lld)", (long long)head_dim);
+  DGG_REQUIRE(tokens >= 0 && tokens <= 0x7fffffff, DGG_ERR_SHAPE, "rotary_cos_sin: bad token count %lld",
+              (long long)tokens);
+  if (tokens == 0) return DGG_OK;
+  DGG_REQUIRE(positions && cos_sin, DGG_ERR_NULL, "rotary_cos_sin: null pointer");
+  const int64_t n = tokens * (head_dim / 2);
+  const unsigned blocks = (unsigned)std::min<int64_t>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(rotary_cos_sin_kernel, dim3(blocks), dim3(256), 0, dgg::as_stream(stream), positions, cos_sin,
+                     tokens, (int)head_dim, rope_theta);
+  return dgg::check_launch("rotary_cos_sin");
+}
+
 extern "C" int dgg_rotary_embedding_online(const int32_t* positions, void* query, void* key, int64_t tokens,
                                            int64_t head_num, int64_t kv_head_num, int64_t head_dim,
                                            int64_t q_row_stride, int64_t k_row_stride, int dtype, float rope_theta,

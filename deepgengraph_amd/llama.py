@@ -4,7 +4,9 @@ The attention block follows LlamaLayer.forward's first half (deepgengraph_exp/ca
 Attention.forward (models/attn.py:34-53): RMSNorm -> fused QKV projection -> rotary on q and k -> causal
 attention -> output projection. The projections are plain library GEMMs (torch.matmul -> hipBLASLt); everything
 else runs in libdgg_hip.so. Unlike the reference, q/k/v are not copied out of the QKV result with
-.contiguous() (models/attn.py:36-39): the rotary and attention kernels take the strided views directly.
+.contiguous() (models/attn.py:36-39): the rotary and attention kernels take the strided views directly. With
+fuse_rope (head_dim 128) the query's rotation runs inside the attention kernel from a per-position (cos, sin)
+table, and the rotary kernel rotates k only: the query never makes the extra round trip through HBM.
 """
 from __future__ import annotations
 
@@ -16,19 +18,28 @@ from . import ops
 
 class LlamaAttentionBlock:
     def __init__(self, w_norm, w_qkv, w_o, *, heads: int, kv_heads: int, eps: float = 1e-6,
-                 rope_theta: float = 10000.0):
+                 rope_theta: float = 10000.0, fuse_rope: bool = True):
         self.w_norm, self.w_qkv, self.w_o = w_norm, w_qkv, w_o
         self.heads, self.kv_heads = heads, kv_heads
         self.hidden = w_o.shape[0]
         self.head_dim = self.hidden // heads
         self.eps, self.theta = eps, rope_theta
+        self.fuse_rope = fuse_rope and self.head_dim == 128 and w_qkv.dtype in (torch.float16, torch.bfloat16)
         self._pos = None
+        self._cs = None
 
     def positions(self, B: int, S: int, device) -> torch.Tensor:
         """Token positions 0..S-1 (models/attn.py:40), repeated for each batch entry."""
         if self._pos is None or self._pos.shape != (B, S) or self._pos.device != device:
             self._pos = torch.arange(S, dtype=torch.int32, device=device).repeat(B, 1).contiguous()
+            self._cs = None
         return self._pos
+
+    def cos_sin(self, pos: torch.Tensor) -> torch.Tensor:
+        """The query rotation table of the positions (computed once per positions tensor)."""
+        if self._cs is None:
+            self._cs = _attn.rotary_cos_sin(pos, self.head_dim, self.theta)
+        return self._cs
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         B, S, _ = x.shape
@@ -39,8 +50,15 @@ class LlamaAttentionBlock:
         q = qkv[..., : H * D]
         k = qkv[..., H * D: (H + Hk) * D]
         v = qkv[..., (H + Hk) * D:]
-        ops.rotary_embedding_online(self.positions(B, S, x.device), q, k, D, self.theta)  # models/attn.py:41
-        o = _attn.attention(q.view(B, S, H, D), k.view(B, S, Hk, D), v.view(B, S, Hk, D), causal=True)
+        pos = self.positions(B, S, x.device)
+        if self.fuse_rope:
+            ops.rotary_embedding_online(pos, k, None, D, self.theta)   # models/attn.py:41, key half
+            cs = self.cos_sin(pos)                                     # query half: inside the attention kernel
+            o = _attn.attention(q.view(B, S, H, D), k.view(B, S, Hk, D), v.view(B, S, Hk, D), causal=True,
+                                rope_cos_sin=cs)
+        else:
+            ops.rotary_embedding_online(pos, q, k, D, self.theta)     # models/attn.py:41
+            o = _attn.attention(q.view(B, S, H, D), k.view(B, S, Hk, D), v.view(B, S, Hk, D), causal=True)
         return torch.matmul(o.view(B, S, H * D), self.w_o.t())         # models/attn.py:52
 
 

@@ -7,7 +7,8 @@ RMSNorm; Llama-2-7B sizes of run_e2e.py:22-43: hidden 4096, 32 heads of 128, MLP
 and random token ids (run_e2e.py:46-90), plugs in the attention callable compile(...) returns for the case
 (run_e2e.py:206-230) and times the forward with the reference's perf() report line (deepgengraph_exp/utils.py:
 50-82; run = warmup = 50, run_e2e.py:241-249). RMSNorm, rotary and SiLU-and-mul run on this library's kernels
-(the csrc ops of llama_base.py:257-314); the projections are torch matmuls. After the attention each model
+(the csrc ops of llama_base.py:257-314), each residual add inside the next RMSNorm (fused_add_rms_norm); the
+projections are torch matmuls. After the attention each model
 compacts its KV cache as its reference model does (top-k of the case's key scores, RoCo's std rule, Corm's
 nonzero); with system 'mi355x' those steps run on this library's kernels (topk_indices, kv_gather, nonzero),
 with 'torch' on torch's. Every model here uses random weights: in the reference only `attn` (and `h2o`) skip
@@ -171,20 +172,40 @@ class Layer(nn.Module):
 
 
 class Llama(nn.Module):
-    """models/attn.py:85-109 (forward: embedding, the layers, final RMSNorm; returns (x, kv_caches))."""
+    """models/attn.py:85-109 (forward: embedding, the layers, final RMSNorm; returns (x, kv_caches)).
 
-    def __init__(self, cfg, attn_f, model, system):
+    With fuse_residual (the default for the 'mi355x' system) each residual add runs inside the RMSNorm that reads
+    its result, as the unexported fused_add_rms_norm of csrc/norm.cu:59-83 / 100-113 does: the add after the
+    attention with the layer's post_layernorm, the add after the MLP with the next layer's input_layernorm (the
+    model's final rms_norm after the last layer). That saves one read and one write of the [S, hidden] residual
+    stream per add. The variance is taken from the fp32 sum before it is rounded to the stored residual
+    (norm.cu:59-83), where the unfused path (models/attn.py:71-80) takes it from the rounded sum."""
+
+    def __init__(self, cfg, attn_f, model, system, fuse_residual=None):
         super().__init__()
         self.embed_tokens = nn.Embedding(cfg.vocab_size, cfg.hidden_size, dtype=cfg.torch_dtype)
         self.layers = nn.ModuleList(Layer(cfg, attn_f, model, system) for _ in range(cfg.num_hidden_layers))
         self.rms_norm = RmsNorm(cfg.hidden_size, cfg.rms_norm_eps, cfg.torch_dtype)
+        self.eps = cfg.rms_norm_eps
+        self.fuse_residual = system != "torch" if fuse_residual is None else bool(fuse_residual)
 
     def forward(self, token_ids):
         kv_caches = []
         x = self.embed_tokens(token_ids)
-        for layer in self.layers:
-            x, kv_caches = layer(x, kv_caches)
-        return self.rms_norm(x), kv_caches
+        if not self.fuse_residual:
+            for layer in self.layers:
+                x, kv_caches = layer(x, kv_caches)
+            return self.rms_norm(x), kv_caches
+        res = x  # the residual stream, updated in place
+        h = self.layers[0].input_layernorm(res) if self.layers else self.rms_norm(res)
+        for i, layer in enumerate(self.layers):
+            a, kv_caches = layer.attention(h, kv_caches)
+            ops.fused_add_rms_norm(a, res, layer.post_layernorm.weight, self.eps)  # res += a; a = norm(res)
+            m = layer.mlp(a)
+            nxt = self.layers[i + 1].input_layernorm if i + 1 < len(self.layers) else self.rms_norm
+            ops.fused_add_rms_norm(m, res, nxt.weight, self.eps)  # res += m; m = norm(res)
+            h = m
+        return h, kv_caches
 
 
 def perf(label, f, args, run=4, warmup=4):
@@ -207,7 +228,7 @@ def perf(label, f, args, run=4, warmup=4):
     return float(np.mean(ms))
 
 
-def build(model: str, system: str, seqlen: int, layer_num: int, seed: int = 0):
+def build(model: str, system: str, seqlen: int, layer_num: int, seed: int = 0, fuse_residual=None):
     """run_e2e.py:197-238: the case module, its compiled attention callable, the random-weight model and the
     random token ids."""
     if model not in KERNEL_ZOO:
@@ -222,7 +243,7 @@ def build(model: str, system: str, seqlen: int, layer_num: int, seed: int = 0):
                          output_names=specs["output"], system=system)
     cfg = E2EConfig(seqlen, layer_num)
     with torch.device("cuda"):
-        net = Llama(cfg, attn_f, model, system)
+        net = Llama(cfg, attn_f, model, system, fuse_residual)
     for p in net.parameters():
         p.requires_grad = False
     token_ids = torch.randint(0, cfg.vocab_size, (1, seqlen), dtype=torch.int64, device="cuda").contiguous()
@@ -238,9 +259,12 @@ def main(argv=None):
     ap.add_argument("--platform", "-p", default="yes", help="accepted for compatibility (it chose checkpoint paths)")
     ap.add_argument("--run", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--no-fuse-residual", action="store_true",
+                    help="residual adds as separate torch adds (models/attn.py:71-80) instead of fused_add_rms_norm")
     a = ap.parse_args(argv)
     print(f"model={a.model!r} system={a.system!r} seqlen={a.seqlen} layer_num={a.layer_num}")
-    net, token_ids = build(a.model, a.system, a.seqlen, a.layer_num)
+    net, token_ids = build(a.model, a.system, a.seqlen, a.layer_num,
+                           fuse_residual=False if a.no_fuse_residual else None)
     print(f"token_ids.shape={tuple(token_ids.shape)}")
     with torch.no_grad():
         return perf(a.system, net, (token_ids,), run=a.run, warmup=a.warmup)

@@ -84,6 +84,11 @@ int dgg_silu_and_mul(void* out, const void* input, int64_t rows, int64_t d, int6
 int dgg_rotary_embedding_online(const int32_t* positions, void* query, void* key, int64_t tokens,
                                 int64_t head_num, int64_t kv_head_num, int64_t head_dim, int64_t q_row_stride,
                                 int64_t k_row_stride, int dtype, float rope_theta, void* stream);
+/* The (cos, sin) table of the online rotary for dgg_attn_prefill_rope (no counterpart in the reference; the values
+ * are those rotary_embedding_online computes, pos_encoding.cu:83-86): cos_sin fp32 [tokens, head_dim], row t =
+ * cos(pos[t] / theta^(2i/head_dim)) for i < head_dim/2, then the sines. */
+int dgg_rotary_cos_sin(const int32_t* positions, float* cos_sin, int64_t tokens, int64_t head_dim, float rope_theta,
+                       void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Attention. The reference has no kernel ABI for attention: it is the callable returned by
@@ -106,6 +111,16 @@ int dgg_rotary_embedding_online(const int32_t* positions, void* query, void* key
 int dgg_attn_prefill(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t Sq,
                      int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides, float scale,
                      float softcap, int64_t window, uint32_t flags, int dtype, void* stream);
+/* dgg_attn_prefill with the query's rotary embedding fused into the kernel (no counterpart as one call in the
+ * reference: it replaces rotary_embedding_online on the query, csrc/pos_encoding.cu:180-199 via models/attn.py:41,
+ * followed by the attention). Row i of batch b of q is rotated by row b * Sq + i of q_cos_sin, fp32
+ * [B * Sq, 128]: the cos of the 64 angles pos / theta^(2j/128) followed by their sines, as dgg_rotary_cos_sin
+ * writes them; the rotated row is rounded to the input dtype before use, as the rotary op stores it. q itself is
+ * not modified. head_dim 128 and f16 / bf16 only; q_cos_sin 32-byte aligned. Other arguments as dgg_attn_prefill. */
+int dgg_attn_prefill_rope(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B, int64_t Sq,
+                          int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, const int64_t* strides, float scale,
+                          float softcap, int64_t window, uint32_t flags, int dtype, const float* q_cos_sin,
+                          void* stream);
 
 /* H2O column sums (deepgengraph_exp/cases/kernels/h2o.py:35-36): colsum[b,h,j] = sum_i p[b,h,i,j] with p
  * the fp32 probabilities of dgg_attn_prefill, recomputed from q, k and the lse it wrote (same scale,

@@ -181,6 +181,24 @@ def test_decode_noalloc_validation(lib):
     assert call(B=0) == OK
 
 
+def test_fused_rotary_validation(lib):
+    assert lib.dgg_rotary_cos_sin(FAKE, FAKE, 16, 100, 1e4, None) == E_UNSUP
+    assert lib.dgg_rotary_cos_sin(None, FAKE, 16, 128, 1e4, None) == E_NULL
+    assert lib.dgg_rotary_cos_sin(None, None, 0, 128, 1e4, None) == OK
+    s = _strides([128 * 512, 512, 128] * 2 + [128 * 256, 256, 128] * 2)
+
+    def call(**kw):
+        a = dict(D=128, dtype=_lib.DGG_BF16, cs=FAKE)
+        a.update(kw)
+        return lib.dgg_attn_prefill_rope(FAKE, FAKE, FAKE, FAKE, None, 1, 128, 128, 4, 2, a["D"], s, 0.088, 0.0, 0, 1,
+                                         a["dtype"], a["cs"], None)
+
+    assert call(D=64) == E_UNSUP             # the reference's rotary is head_dim 128 only (pos_encoding.cu:195)
+    assert call(dtype=_lib.DGG_F32) == E_UNSUP
+    assert call(cs=None) == E_NULL
+    assert call(cs=ctypes.c_void_p(0x10010)) == E_ALIGN
+
+
 def test_clock_probe_validation(lib):
     assert lib.dgg_clock_probe(None, 100, None) == E_NULL
     assert lib.dgg_clock_probe(ctypes.c_void_p(0x10004), 100, None) == E_ALIGN

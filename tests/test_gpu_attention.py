@@ -188,6 +188,57 @@ def test_prefill_golden(gpu, name, kw, dtype):
     assert_close(lse.cpu(), torch.from_numpy(g["lse"]), 2e-2, 1e-2, name + " lse")
 
 
+@pytest.mark.parametrize("B,Sq,Sk,Hq,Hkv,dtype,causal", [
+    (1, 512, 512, 4, 4, torch.bfloat16, True),
+    (2, 300, 300, 4, 2, torch.float16, True),     # GQA, ragged, batch-major table rows
+    (1, 130, 700, 2, 2, torch.bfloat16, True),    # Sq < Sk
+    (1, 257, 257, 2, 2, torch.float16, False),
+])
+def test_prefill_fused_query_rotary_matches_oracle(gpu, B, Sq, Sk, Hq, Hkv, dtype, causal):
+    # attention(rope_cos_sin=...) on the unrotated q equals the oracle's rotary (pos_encoding.cu:64-113) of q followed
+    # by the oracle attention; k is rotated beforehand as the block does; q is left unmodified
+    from oracle import elementwise as oe
+
+    q, k, v = _qkv(B, Sq, Sk, Hq, Hkv, 128, dtype, seed=Sq + 31 * Sk)
+    pos = torch.arange(Sq, dtype=torch.int32).repeat(B) + (Sk - Sq)  # the query rows' positions
+    q_rot, _ = oe.rotary_embedding_online(pos, q.reshape(B * Sq, Hq * 128), None, 128, 10000.0)
+    ref = oa.attention(q_rot.view(B, Sq, Hq, 128), k, v, causal=causal)
+    qg = q.to(gpu)
+    cs = A.rotary_cos_sin(pos.to(gpu).contiguous(), 128, 10000.0)
+    out = A.attention(qg, k.to(gpu), v.to(gpu), causal=causal, rope_cos_sin=cs)
+    what = f"fused rotary B{B} Sq{Sq} Sk{Sk} H{Hq}/{Hkv} {dtype} causal={causal}"
+    assert_close(out.cpu().float(), ref.float(), *TOL[dtype], what)
+    assert torch.equal(qg.cpu(), q), "q must not be modified"
+    # against the unfused GPU path (the rotary kernel on q, then attention): the table holds the rotary kernel's
+    # own angles, so the two differ at most by the rounding of a multiply-add
+    from deepgengraph_amd import ops
+
+    q2 = qg.clone()
+    ops.rotary_embedding_online(pos.to(gpu).contiguous(), q2.view(B * Sq, Hq * 128), None, 128, 10000.0)
+    plain = A.attention(q2, k.to(gpu), v.to(gpu), causal=causal)
+    assert_close(out.cpu().float(), plain.cpu().float(), *TOL[torch.float16], what + " vs unfused")
+    # the table against float angles of the oracle (fp32 angles of positions ~1e3 carry ~1e-4 rad of rounding)
+    oc, os_ = oe.rotary_cos_sin(pos, 128, 10000.0)
+    assert_close(cs.cpu()[:, :64], oc, 2e-4, 0, what + " cos table")
+    assert_close(cs.cpu()[:, 64:], os_, 2e-4, 0, what + " sin table")
+
+
+def test_llama_block_fused_rotary_matches_unfused(gpu):
+    # the config-2 block with the query rotation inside the attention kernel against the unfused block
+    from deepgengraph_amd.llama import LlamaAttentionBlock
+
+    g = torch.Generator().manual_seed(8)
+    hidden, heads, S = 1024, 8, 384
+    x = torch.randn(1, S, hidden, generator=g).bfloat16().to(gpu)
+    w_norm = (1 + 0.02 * torch.randn(hidden, generator=g)).bfloat16().to(gpu)
+    w_qkv = (0.02 * torch.randn(3 * hidden, hidden, generator=g)).bfloat16().to(gpu)
+    w_o = (0.02 * torch.randn(hidden, hidden, generator=g)).bfloat16().to(gpu)
+    fused = LlamaAttentionBlock(w_norm, w_qkv, w_o, heads=heads, kv_heads=heads, fuse_rope=True)
+    plain = LlamaAttentionBlock(w_norm, w_qkv, w_o, heads=heads, kv_heads=heads, fuse_rope=False)
+    assert fused.fuse_rope and not plain.fuse_rope
+    assert_close(fused(x).cpu().float(), plain(x).cpu().float(), 2e-2, 1e-2, "fused vs unfused block")
+
+
 def test_prefill_strided_views(gpu):
     # q/k/v as column slices of one fused QKV activation (row stride 3*H*D), output into a strided view
     S, H, D = 320, 4, 128

@@ -51,6 +51,19 @@ def test_e2e_matches_torch_attention(gpu, model):
         assert same > 0.9, f"{model}: only {same:.3f} of the kept (key, head) rows agree"
 
 
+def test_e2e_fused_residual_matches_unfused(gpu):
+    # the residual adds inside fused_add_rms_norm (csrc/norm.cu:59-83) against separate adds (models/attn.py:71-80)
+    x = {}
+    for fuse in (True, False):
+        net, ids = run_e2e.build("attn", "mi355x", 1024, 2, seed=0, fuse_residual=fuse)
+        assert net.fuse_residual == fuse
+        with torch.no_grad():
+            x[fuse] = net(ids)[0]
+    assert torch.isfinite(x[True]).all()
+    assert torch.allclose(x[True].float(), x[False].float(), atol=2e-2, rtol=2e-2), \
+        f"max |diff| {(x[True].float() - x[False].float()).abs().max().item()}"
+
+
 def test_e2e_cli_llama2_7b(gpu, capsys):
     # the reference's default workload: Llama-2-7B sizes, 32 layers, 4096 tokens (a few timed runs)
     ms = run_e2e.main(["-m", "attn", "-s", "mi355x", "--run", "3", "--warmup", "2"])

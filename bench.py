@@ -114,6 +114,11 @@ def bench_prefill(args, dev):
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     kern_ms = start.elapsed_time(end) / args.steps
     _clock_probe(dev, clk, 1)
+    flops = cfg.reference_flops()
+    if args.no_steady:
+        return dict(cfg=cfg, wall_ms=wall_ms, kern_ms=kern_ms, flops=flops, exact_flops=cfg.flops(),
+                    tflops_wall=flops / (wall_ms * 1e-3) / 1e12, tflops_kern=flops / (kern_ms * 1e-3) / 1e12,
+                    clock_mhz=[_clock_mhz(clk, 0), _clock_mhz(clk, 1)], steady=None)
     # steady figure (not `value`): top the launches up to STEADY_WARMUP, then time STEADY_STEPS more
     for _ in range(max(0, STEADY_WARMUP - args.warmup - args.steps)):
         fn()
@@ -126,7 +131,6 @@ def bench_prefill(args, dev):
     _clock_probe(dev, clk, 3)
     torch.cuda.synchronize()
     steady_ms = s0.elapsed_time(s1) / STEADY_STEPS
-    flops = cfg.reference_flops()
     steady = dict(warmup_launches=max(STEADY_WARMUP, args.warmup + args.steps), steps=STEADY_STEPS,
                   kernel_ms=round(steady_ms, 5), tflops=round(flops / (steady_ms * 1e-3) / 1e12, 2),
                   frac=round(flops / (steady_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
@@ -326,6 +330,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--sections", default="prefill,decode,prestep,variants,block")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-steady", action="store_true", help="skip the steady-clock figure (short profiled runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build measures one GPU only (the attention hot path runs on a single GPU; multi-GPU "

@@ -296,8 +296,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   constexpr int NKK = D / 16;
   constexpr int NMB = BN / 32;
   constexpr int CPT = BN * D / 8 / kThreads;  // 16-byte chunks per thread per tile
-  constexpr int TPR = (D / 8) / CPT;          // threads per key row
-  static_assert(CPT * kThreads == BN * D / 8 && kThreads / TPR == BN, "tile mapping");
+  static_assert(CPT * kThreads == BN * D / 8, "tile mapping");
   __shared__ __attribute__((aligned(16))) S Ks[2][BN][KP];
 
   int qt, bh;
@@ -331,17 +330,25 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   if (p.causal) k_hi = min(k_hi, qi + p.offset);
   if (p.window > 0) k_lo = max(k_lo, qi + p.offset - p.window + 1);
 
-  // K staging: thread tid copies CPT adjacent chunks of key row tid / TPR (rows past the end read the last row).
+  // K staging: copy i of thread tid moves 16-byte chunk (tid + i * kThreads) of the tile, i.e. chunk c % (D/8) of
+  // key row c / (D/8) (rows past the end read the last row). Consecutive lanes take consecutive chunks of a row, so
+  // each store instruction writes whole rows and the lanes of one LDS pass hit distinct banks (a thread writing
+  // CPT adjacent chunks, one instruction per chunk, put lanes 128 bytes apart on the same banks).
   V8 kreg[CPT];
-  const int k_row0 = tid / TPR, k_c0 = (tid % TPR) * CPT;
+  constexpr int CPR = D / 8;  // chunks per key row
   auto load = [&](int t) {
-    const S* src = kp + (int64_t)min(t * BN + k_row0, p.Sk - 1) * p.k_ss + k_c0 * 8;
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) kreg[i] = ld16<V8>(src + 8 * i);
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + i * kThreads;
+      kreg[i] = ld16<V8>(kp + (int64_t)min(t * BN + c / CPR, p.Sk - 1) * p.k_ss + (c % CPR) * 8);
+    }
   };
   auto store = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) *reinterpret_cast<V8*>(&Ks[buf][k_row0][(k_c0 + i) * 8]) = kreg[i];
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + i * kThreads;
+      *reinterpret_cast<V8*>(&Ks[buf][c / CPR][(c % CPR) * 8]) = kreg[i];
+    }
   };
 
   const float c = score_coeff<false, REFROUND>(p);

@@ -233,6 +233,11 @@ def bench_variants(args, dev):
     res["cfg4_h2o_fwd_colsum_topk"] = dict(ms=round(ms, 4),
                                            tflops=round(cfg.reference_flops() / (ms * 1e-3) / 1e12, 1),
                                            frac=round(cfg.reference_flops() / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))
+    cs = A.h2o_attention(q, k, v)[1]
+    ms = _events_time(lambda: A.topk_indices(cs, cfg.topk), 20, 2)
+    ms_t = _events_time(lambda: torch.topk(cs, k=cfg.topk, dim=-1, sorted=True)[1].sort(dim=-1)[0], 20, 2)
+    res["cfg4_topk256"] = dict(us=round(ms * 1e3, 2), torch_us=round(ms_t * 1e3, 2))
+    del cs
     # the other selection cases of the reference at config-4 shapes (same inputs; Corm's threshold 1/(i+1))
     thr = torch.ones(cfg.Sq, cfg.Sk, device=dev) / torch.arange(1, cfg.Sq + 1, device=dev, dtype=torch.float32)[:, None]
     for name, fn in (("cfg4_roco", lambda: A.roco_attention(q, k, v)),
@@ -248,6 +253,24 @@ def bench_variants(args, dev):
     res["cfg4_keyformer"] = dict(ms=round(ms, 4), tflops=round(cfg.reference_flops() / (ms * 1e-3) / 1e12, 1),
                                  exp_rand_gbps=round(er_bytes / (ms * 1e-3) / 1e9, 1))
     del er
+    # RoCo's selection (models/roco.py:54-61) over the config-4 column sums with the e2e model's budget (512) and
+    # recent window (256): the fused kernel against the reference's torch lines on the same GPU
+    _, s1, s2 = A.roco_attention(q, k, v)
+    S = cfg.Sk
+
+    def roco_torch():
+        std = torch.sqrt(s2 / S - (s1 / S) ** 2)
+        other = torch.topk(std, largest=False, k=S - 256, dim=-1)[1]
+        recent = torch.topk(std, largest=True, k=256, dim=-1)[1]
+        pick = torch.topk(s1.gather(dim=-1, index=other) / S, dim=-1, k=512)[1]
+        return torch.cat([other.gather(dim=-1, index=pick), recent], dim=-1).sort(dim=-1)[0]
+
+    ms = _events_time(lambda: A.roco_select(s1, s2, S, 256, 512), 20, 2)
+    ms_t = _events_time(roco_torch, 20, 2)
+    nb = 2 * s1.numel() * 4 + s1.numel() // S * 768 * 8  # both sums read once, 768 indices written per row
+    res["cfg4_roco_select"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1),
+                                   torch_us=round(ms_t * 1e3, 2))
+    del s1, s2
     idx = A.topk_indices(A.h2o_attention(q, k, v)[1], cfg.topk)
     ms = _events_time(lambda: A.kv_gather(k, v, idx), 20, 2)
     nb = 2 * 2 * idx.numel() * cfg.D * k.element_size()  # K and V rows read once and written once

@@ -317,17 +317,38 @@ def nonzero(x: torch.Tensor) -> torch.Tensor:
     return coords[: int(total.item())]
 
 
-def topk_indices(scores: torch.Tensor, k: int) -> torch.Tensor:
+def topk_indices(scores: torch.Tensor, k: int, largest: bool = True) -> torch.Tensor:
     """deepgengraph_exp/cases/models/h2o.py:51-52 (torch.topk then sort of the indices) with a defined tie
-    order: the k largest of each row of scores [..., n] (fp32), ties broken by the lowest index, returned as int64
-    indices [..., k] in ascending order."""
+    order: the k largest (largest=False: smallest, models/roco.py:55) of each row of scores [..., n] (fp32), ties
+    broken by the lowest index, NaN ranked above +inf as torch.topk ranks it, returned as int64 indices [..., k] in
+    ascending order."""
     dev = _lib.require_gpu(scores)
     if scores.dtype != torch.float32 or not scores.is_contiguous():
         raise RuntimeError("topk_indices: scores must be a contiguous fp32 tensor")
     n = scores.shape[-1]
     rows = scores.numel() // n if n else 0
     out = torch.empty(*scores.shape[:-1], k, dtype=torch.int64, device=scores.device)
-    _lib.call("dgg_topk_indices", _lib.ptr(scores), rows, n, int(k), _lib.ptr(out), _lib.stream_handle(dev))
+    _lib.call("dgg_topk_select", _lib.ptr(scores), rows, n, int(k), 1 if largest else 0, _lib.ptr(out),
+              _lib.stream_handle(dev))
+    return out
+
+
+def roco_select(score: torch.Tensor, sq_score: torch.Tensor, q_len: int, recent: int, budget: int) -> torch.Tensor:
+    """RoCo's KV selection, deepgengraph_exp/cases/models/roco.py:54-61, in one kernel: std of each key's
+    probabilities from roco_score / roco_sq_score [..., n] (fp32, rounded as torch rounds it on the GPU), the
+    `recent` keys of largest std plus the `budget` keys of largest roco_score among the n - recent of smallest std,
+    as int64 indices [..., budget + recent] in ascending order (ties: lowest index first)."""
+    dev = _lib.require_gpu(score)
+    for t in (score, sq_score):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise RuntimeError("roco_select: scores must be contiguous fp32 tensors")
+    if sq_score.shape != score.shape or sq_score.device != score.device:
+        raise RuntimeError(f"roco_select: score {tuple(score.shape)} and sq_score {tuple(sq_score.shape)} differ")
+    n = score.shape[-1]
+    rows = score.numel() // n if n else 0
+    out = torch.empty(*score.shape[:-1], budget + recent, dtype=torch.int64, device=score.device)
+    _lib.call("dgg_roco_select", _lib.ptr(score), _lib.ptr(sq_score), rows, n, int(q_len), int(recent), int(budget),
+              _lib.ptr(out), _lib.stream_handle(dev))
     return out
 
 

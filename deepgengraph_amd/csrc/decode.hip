@@ -1,4 +1,4 @@
-// Decode attention (one query token per sequence) as split-KV + log-sum-exp merge, and the H2O top-k.
+// Decode attention (one query token per sequence) as split-KV + log-sum-exp merge.
 //
 // Decode is HBM-bound: each (batch, head, split) workgroup streams its slice of the K and V caches once
 // with 16-byte loads. Lanes are grouped D/8 per key row, so one wave instruction covers 512/D whole
@@ -165,119 +165,6 @@ void launch_decode(const DecodeParams& p, hipStream_t st) {
   hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(p.Hq, p.B), dim3(D < 256 ? 128 : 256), 0, st, p);
 }
 
-// ------------------------------------------------------------------------------------------------
-// Top-k with lowest-index tie-break (one 1024-thread workgroup per row). Radix select over an
-// order-preserving 32-bit key (4 passes of 8 bits) finds the k-th largest key K*; every element with
-// key > K* is taken, plus the lowest-indexed elements equal to K* until k are taken. Each thread owns a
-// contiguous index segment, so block-wide exclusive scans give both the tie ranks and the output
-// positions in ascending index order.
-// ------------------------------------------------------------------------------------------------
-constexpr int kTopkThreads = 1024;
-
-__device__ __forceinline__ uint32_t order_key(float x) {
-  uint32_t u = __float_as_uint(x == 0.f ? 0.f : x);  // -0.0 == +0.0
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-// Block-wide exclusive scan of one uint32 per thread (1024 threads = 16 waves).
-__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wsum, uint32_t& total) {
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  uint32_t inc = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t t = __shfl_up(inc, off, 64);
-    if (lane >= off) inc += t;
-  }
-  if (lane == 63) wsum[wid] = inc;
-  __syncthreads();
-  uint32_t before = 0, all = 0;
-  for (int i = 0; i < kTopkThreads / 64; ++i) {
-    const uint32_t s = wsum[i];
-    if (i < wid) before += s;
-    all += s;
-  }
-  __syncthreads();
-  total = all;
-  return before + inc - v;
-}
-
-// PER: elements per thread kept in registers (n <= PER * 1024). Histograms are per wave (no atomics
-// shared across waves); the digit of each pass is found by a 256-thread suffix scan over the bins.
-template <int PER>
-__global__ void __launch_bounds__(kTopkThreads) topk_kernel(const float* __restrict__ scores, int n, int k,
-                                                             int64_t* __restrict__ out) {
-  constexpr int NWV = kTopkThreads / 64;
-  __shared__ uint32_t hist[NWV][256];
-  __shared__ uint32_t wsum[NWV];
-  __shared__ uint32_t sel_digit, sel_remaining;
-  const float* x = scores + (int64_t)blockIdx.x * n;
-  int64_t* o = out + (int64_t)blockIdx.x * k;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int per = (n + kTopkThreads - 1) / kTopkThreads;
-  const int seg0 = min(n, tid * per), cnt = min(n, seg0 + per) - seg0;
-
-  uint32_t key[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) key[j] = j < cnt ? order_key(x[seg0 + j]) : 0u;
-
-  uint32_t prefix = 0, pmask = 0, remaining = (uint32_t)k;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int i = tid; i < NWV * 256; i += kTopkThreads) (&hist[0][0])[i] = 0u;
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < PER; ++j)
-      if (j < cnt && (key[j] & pmask) == prefix) atomicAdd(&hist[wv][(key[j] >> shift) & 255u], 1u);
-    __syncthreads();
-    // Thread t < 256 takes bin 255 - t: an inclusive scan over t counts the candidates in bins >= 255 - t.
-    uint32_t c = 0, incl = 0;
-    if (tid < 256) {
-#pragma unroll
-      for (int w2 = 0; w2 < NWV; ++w2) c += hist[w2][255 - tid];
-      incl = c;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t t = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += t;
-      }
-      if (lane == 63) wsum[wv] = incl;
-    }
-    __syncthreads();
-    if (tid < 256) {
-      uint32_t base = 0;
-      for (int w2 = 0; w2 < wv; ++w2) base += wsum[w2];
-      const uint32_t hi = base + incl, lo = hi - c;  // candidates in bins above / from this bin
-      if (lo < remaining && hi >= remaining) {      // exactly one bin: the k-th largest lies in it
-        sel_digit = 255u - (uint32_t)tid;
-        sel_remaining = remaining - lo;
-      }
-    }
-    __syncthreads();
-    prefix |= sel_digit << shift;
-    pmask |= 255u << shift;
-    remaining = sel_remaining;
-  }
-  // prefix = K*; `remaining` elements equal to K* are still to be taken, lowest index first.
-  uint32_t eq = 0, gt = 0;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    eq += j < cnt && key[j] == prefix;
-    gt += j < cnt && key[j] > prefix;
-  }
-  uint32_t tot;
-  const uint32_t eq_before = block_exclusive_scan(eq, wsum, tot);
-  const uint32_t eq_take = eq_before >= remaining ? 0u : min(eq, remaining - eq_before);
-  uint32_t pos = block_exclusive_scan(gt + eq_take, wsum, tot);
-  uint32_t eq_seen = eq_before;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    if (j < cnt) {
-      bool take = key[j] > prefix;
-      if (key[j] == prefix) take = eq_seen++ < remaining;
-      if (take && pos < (uint32_t)k) o[pos++] = seg0 + j;
-    }
-  }
-}
-
 }  // namespace
 
 extern "C" int64_t dgg_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_t splits) {
@@ -411,20 +298,4 @@ extern "C" int dgg_attn_decode_noalloc(const void* q, const void* k, const void*
                                        int64_t splits, float scale, int dtype, void* stream) {
   return decode_impl("attn_decode_noalloc", q, k, v, o, lse, nullptr, kDecodeScratchBytes, B, Hq, Hkv, L, D, strides,
                      splits, scale, dtype, stream, true);
-}
-
-extern "C" int dgg_topk_indices(const float* scores, int64_t rows, int64_t n, int64_t k, int64_t* out_idx,
-                                void* stream) {
-  DGG_REQUIRE(rows >= 0 && rows < (1ll << 31), DGG_ERR_SHAPE, "topk_indices: bad row count %lld", (long long)rows);
-  DGG_REQUIRE(n >= 1 && n <= 65536, DGG_ERR_SHAPE, "topk_indices: n must be in [1, 65536] (got %lld)", (long long)n);
-  DGG_REQUIRE(k >= 1 && k <= n, DGG_ERR_SHAPE, "topk_indices: k must be in [1, n] (got k=%lld, n=%lld)",
-              (long long)k, (long long)n);
-  if (rows == 0) return DGG_OK;
-  DGG_REQUIRE(scores && out_idx, DGG_ERR_NULL, "topk_indices: null pointer");
-  const dim3 grid((unsigned)rows), block(kTopkThreads);
-  hipStream_t st = dgg::as_stream(stream);
-  if (n <= 4 * kTopkThreads) hipLaunchKernelGGL(topk_kernel<4>, grid, block, 0, st, scores, (int)n, (int)k, out_idx);
-  else if (n <= 16 * kTopkThreads) hipLaunchKernelGGL(topk_kernel<16>, grid, block, 0, st, scores, (int)n, (int)k, out_idx);
-  else hipLaunchKernelGGL(topk_kernel<64>, grid, block, 0, st, scores, (int)n, (int)k, out_idx);
-  return dgg::check_launch("topk_indices");
 }

@@ -139,11 +139,14 @@ class Attention(nn.Module):
             kv_caches.append((score, self._select(self._topk(score, cfg.cache_budget), k4, v4)))
         elif self.model == "roco":  # models/roco.py: std of the probabilities, recent window plus top budget
             out, s1, s2 = self.attn_f(q4, k4, v4)
-            std = torch.sqrt(s2 / S - (s1 / S) ** 2)
-            other = torch.topk(std, largest=False, k=S - cfg.roco_recent, dim=-1)[1]
-            recent = torch.topk(std, largest=True, k=cfg.roco_recent, dim=-1)[1]
-            pick = torch.topk(s1.gather(dim=-1, index=other) / S, dim=-1, k=cfg.cache_budget)[1]
-            idx = torch.cat([other.gather(dim=-1, index=pick), recent], dim=-1).sort(dim=-1)[0]
+            if self.system == "torch":
+                std = torch.sqrt(s2 / S - (s1 / S) ** 2)
+                other = torch.topk(std, largest=False, k=S - cfg.roco_recent, dim=-1)[1]
+                recent = torch.topk(std, largest=True, k=cfg.roco_recent, dim=-1)[1]
+                pick = torch.topk(s1.gather(dim=-1, index=other) / S, dim=-1, k=cfg.cache_budget)[1]
+                idx = torch.cat([other.gather(dim=-1, index=pick), recent], dim=-1).sort(dim=-1)[0]
+            else:
+                idx = A.roco_select(s1.contiguous(), s2.contiguous(), S, cfg.roco_recent, cfg.cache_budget)
             kv_caches.append((s1, s2, self._select(idx, k4, v4)))
         elif self.model == "corm":  # models/corm.py: the flagged (head, key) pairs, as torch.nonzero lists them
             out, score = self.attn_f(q4, k4, v4, cfg.corm_mask[:S, :S].contiguous())

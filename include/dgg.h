@@ -189,9 +189,26 @@ int dgg_nonzero(const uint8_t* in, int ndim, const int64_t* dims, int64_t* coord
 
 /* Top-k of H2O scores (deepgengraph_exp/cases/models/h2o.py:51-52: torch.topk then sort of the indices):
  * for each of `rows` rows of n fp32 scores (row stride n), the k largest, ties broken by the lowest index,
- * written as int64 indices in ascending index order to out_idx [rows, k]. -0.0 equals +0.0; NaN is not
- * supported. n <= 65536. */
+ * written as int64 indices in ascending index order to out_idx [rows, k]. Values are ordered as torch.topk
+ * orders them: -0.0 equals +0.0 and NaN (either sign) ranks above +inf. 1 <= k <= n <= 65536. */
 int dgg_topk_indices(const float* scores, int64_t rows, int64_t n, int64_t k, int64_t* out_idx, void* stream);
+
+/* dgg_topk_indices in either direction: largest != 0 is dgg_topk_indices; largest == 0 takes the k smallest
+ * (torch.topk(..., largest=False), deepgengraph_exp/cases/models/roco.py:55), NaN last, ties again broken by the
+ * lowest index. Output in ascending index order. */
+int dgg_topk_select(const float* scores, int64_t rows, int64_t n, int64_t k, int largest, int64_t* out_idx,
+                    void* stream);
+
+/* RoCo's KV selection (deepgengraph_exp/cases/models/roco.py:54-61) for `rows` rows of n keys: from the column sums
+ * score = roco_score and sq_score = roco_sq_score (fp32, row stride n), std = sqrt(sq_score / q_len -
+ * (score / q_len) ** 2) rounded as torch computes it on the GPU (division by q_len = multiplication by the fp32
+ * reciprocal, correctly rounded sqrt, NaN where cancellation makes the variance negative); recent = the `recent`
+ * keys of largest std, other = the n - recent keys of smallest std, pick = the `budget` keys of other with the
+ * largest score / q_len. out_idx [rows, budget + recent] receives pick and recent merged in ascending index order
+ * (an index in both, possible only through ties, appears twice, as the reference's cat + sort keeps it). Ties are
+ * broken by the lowest index in every selection. 0 <= recent <= n <= 65536, 0 <= budget <= n - recent. */
+int dgg_roco_select(const float* score, const float* sq_score, int64_t rows, int64_t n, int64_t q_len, int64_t recent,
+                    int64_t budget, int64_t* out_idx, void* stream);
 
 /* Decode attention (Attn.forward with q_len == 1, attn.py:22-23: no mask) as split-KV + LSE merge.
  * q [B, Hq, D] strides {b,h}; k/v cache [B, Hkv, L, D] strides {b,h,l}; o [B, Hq, D] strides {b,h}.

@@ -165,13 +165,22 @@ def rotary(pos, x, head_dim, theta):
     return out
 
 
-def topk_indices(row, k):
-    """Definition by exhaustive ranking: element i outranks j iff x_i > x_j or (x_i == x_j and i < j);
-    the k elements outranked by fewer than k others, in ascending index order."""
+def topk_indices(row, k, largest=True):
+    """Definition by exhaustive ranking: with NaN ranked above every number and all NaN equal, element i outranks
+    j iff it comes first in the direction (larger when largest, else smaller) or they are equal and i < j; the k
+    elements outranked by fewer than k others, in ascending index order."""
+    def first(a, b):  # a strictly before b in the direction
+        if math.isnan(a) or math.isnan(b):
+            return math.isnan(a) and not math.isnan(b) if largest else math.isnan(b) and not math.isnan(a)
+        return a > b if largest else a < b
+
+    def equal(a, b):
+        return (math.isnan(a) and math.isnan(b)) or a == b
+
     n = len(row)
     sel = []
     for i in range(n):
-        rank = sum(1 for j in range(n) if row[j] > row[i] or (row[j] == row[i] and j < i))
+        rank = sum(1 for j in range(n) if first(row[j], row[i]) or (equal(row[j], row[i]) and j < i))
         if rank < k:
             sel.append(i)
     return sel

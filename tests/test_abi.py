@@ -157,6 +157,25 @@ def test_topk_validation(lib):
     assert lib.dgg_topk_indices(FAKE, 4, 70000, 10, FAKE, None) == E_SHAPE
     assert lib.dgg_topk_indices(None, 4, 100, 10, FAKE, None) == E_NULL
     assert lib.dgg_topk_indices(None, 0, 100, 10, None, None) == OK
+    for largest in (0, 1):
+        assert lib.dgg_topk_select(FAKE, 4, 100, 0, largest, FAKE, None) == E_SHAPE
+        assert lib.dgg_topk_select(FAKE, 4, 0, 1, largest, FAKE, None) == E_SHAPE
+        assert lib.dgg_topk_select(FAKE, 4, 65537, 10, largest, FAKE, None) == E_SHAPE
+        assert lib.dgg_topk_select(FAKE, 4, 100, 10, largest, None, None) == E_NULL
+        assert lib.dgg_topk_select(None, 0, 100, 10, largest, None, None) == OK
+
+
+def test_roco_select_validation(lib):
+    # score, sq_score, rows, n, q_len, recent, budget, out
+    assert lib.dgg_roco_select(FAKE, FAKE, 4, 0, 10, 0, 0, FAKE, None) == E_SHAPE
+    assert lib.dgg_roco_select(FAKE, FAKE, 4, 70000, 10, 0, 1, FAKE, None) == E_SHAPE
+    assert lib.dgg_roco_select(FAKE, FAKE, 4, 100, 0, 10, 10, FAKE, None) == E_SHAPE
+    assert lib.dgg_roco_select(FAKE, FAKE, 4, 100, 100, 101, 0, FAKE, None) == E_SHAPE
+    assert lib.dgg_roco_select(FAKE, FAKE, 4, 100, 100, -1, 0, FAKE, None) == E_SHAPE
+    assert lib.dgg_roco_select(FAKE, FAKE, 4, 100, 100, 30, 71, FAKE, None) == E_SHAPE  # budget > n - recent
+    assert lib.dgg_roco_select(FAKE, None, 4, 100, 100, 30, 70, FAKE, None) == E_NULL
+    assert lib.dgg_roco_select(None, None, 0, 100, 100, 30, 70, None, None) == OK
+    assert lib.dgg_roco_select(None, None, 4, 100, 100, 0, 0, None, None) == OK    # nothing to select
 
 
 def test_decode_noalloc_validation(lib):

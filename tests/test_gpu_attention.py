@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import assert_close, load_golden
+from conftest import assert_close, load_golden, progress
 from deepgengraph_amd import attention as A
 from deepgengraph_amd.compile import compile as dgg_compile
 from oracle import attention as oa
@@ -26,6 +26,14 @@ def _qkv(B, Sq, Sk, Hq, Hkv, D, dtype, seed):
     k = torch.randn(B, Sk, Hkv, D, generator=g).to(dtype)
     v = torch.randn(B, Sk, Hkv, D, generator=g).to(dtype)
     return q, k, v
+
+
+def _qkv_sinks(S, H, D, seed, sinks=16, dtype=torch.float16):
+    """Self-attention inputs [1, S, H, D] with a few attention-sink keys (scaled up), as the H2O tests draw them."""
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(1, S, H, D, generator=g) for _ in range(3))
+    k[:, torch.randperm(S, generator=g)[:sinks]] *= 4.0
+    return q.to(dtype), k.to(dtype), v.to(dtype)
 
 
 CASES = [
@@ -345,6 +353,83 @@ def test_topk_kernel_golden_and_ties(gpu):
         vals[1, ::2] = -0.0
         got = A.topk_indices(torch.from_numpy(vals).to(gpu), k).cpu().numpy()
         np.testing.assert_array_equal(got, osel.topk_indices(vals, k), err_msg=f"n={n} k={k}")
+
+
+def test_topk_smallest_and_nan_order(gpu):
+    # both directions (models/roco.py:55 takes the smallest) on rows with ties, signed zeros, infinities and NaNs,
+    # across the three per-thread segment sizes of the kernel
+    rng = np.random.default_rng(7)
+    pool = np.array([0.0, -0.0, 1.0, -1.0, 2.5, -7.0, np.inf, -np.inf, np.nan, -np.nan], dtype=np.float32)
+    for n, k in ((3, 2), (100, 37), (4096, 4000), (5000, 1), (16384, 9000), (65536, 1000), (40000, 39999)):
+        progress(f"topk both directions n={n} k={k}")
+        vals = rng.integers(0, 1 << 12, size=(4, n)).astype(np.float32) / 64.0 - 30.0
+        vals[1] = rng.choice(pool, size=n)
+        vals[2, ::3] = np.nan
+        vals[3] = rng.integers(0, 3, size=n).astype(np.float32)
+        x = torch.from_numpy(vals).to(gpu)
+        for largest in (True, False):
+            got = A.topk_indices(x, k, largest=largest).cpu().numpy()
+            np.testing.assert_array_equal(got, osel.topk_indices(vals, k, largest), err_msg=f"n={n} k={k} {largest}")
+
+
+def _roco_torch_gpu(s1, s2, q_len, recent, budget):
+    """models/roco.py:54-61 as the reference writes it, run by torch on the GPU (its rounding of / q_len)."""
+    std = torch.sqrt(s2 / q_len - (s1 / q_len) ** 2)
+    _, other = torch.topk(std, largest=False, k=s1.shape[-1] - recent, dim=-1)
+    _, rec = torch.topk(std, largest=True, k=recent, dim=-1)
+    _, pick = torch.topk(s1.gather(dim=-1, index=other) / q_len, dim=-1, k=budget)
+    return torch.cat([other.gather(dim=-1, index=pick), rec], dim=-1).sort(dim=-1)[0]
+
+
+def _boundary_tied(vals, k, largest):
+    """Per row: whether the k-th and (k+1)-th values in the direction are equal (torch's choice is then
+    unspecified)."""
+    nrows = int(np.prod(vals.shape[:-1]))
+    if k == 0 or k >= vals.shape[-1]:
+        return np.zeros(nrows, bool)
+    rows = vals.reshape(nrows, vals.shape[-1])
+    s = np.sort(np.where(np.isnan(rows), np.inf, rows), axis=-1)
+    if largest:
+        s = s[..., ::-1]
+    return s[:, k - 1] == s[:, k]
+
+
+@pytest.mark.parametrize("S,H,recent,budget", [(1024, 4, 256, 512), (4096, 2, 256, 1024), (300, 3, 0, 100),
+                                                (300, 3, 300, 0), (5000, 2, 17, 4983)])
+def test_roco_select_matches_oracle_and_torch(gpu, S, H, recent, budget):
+    # the column sums of a real RoCo forward (fp16 inputs with attention sinks), then the selection of roco.py:54-61
+    progress(f"roco_select S{S} H{H} recent{recent} budget{budget}")
+    q, k, v = (t.to(gpu) for t in _qkv_sinks(S, H, 128, S + recent))
+    _, s1, s2 = A.roco_attention(q, k, v)
+    got = A.roco_select(s1, s2, S, recent, budget)
+    assert got.shape == (1, H, budget + recent)
+    np.testing.assert_array_equal(got.cpu().numpy(),
+                                  osel.roco_select(s1.cpu().numpy(), s2.cpu().numpy(), S, recent, budget))
+    # against torch on the GPU, on every row where its topk has no tie at a selection boundary
+    std = torch.sqrt(s2 / S - (s1 / S) ** 2).cpu().numpy()
+    other = torch.topk(torch.from_numpy(std), largest=False, k=S - recent, dim=-1)[1]
+    picked = np.take_along_axis(s1.cpu().numpy(), other.numpy(), -1) * (np.float32(1) / np.float32(S))
+    tied = _boundary_tied(std, recent, True) | _boundary_tied(std, S - recent, False) | \
+        _boundary_tied(picked, budget, True)
+    assert (~tied).sum() >= H - 1, f"{int(tied.sum())} of {H} rows tie at a selection boundary"
+    ref = _roco_torch_gpu(s1, s2, S, recent, budget).cpu().numpy().reshape(H, -1)
+    np.testing.assert_array_equal(got.cpu().numpy().reshape(H, -1)[~tied], ref[~tied])
+
+
+def test_roco_select_ties_nan_and_edges(gpu):
+    # quantised sums: ties everywhere, and s2 < s1^2 / q_len (negative variance: NaN std) in places
+    rng = np.random.default_rng(5)
+    for n, q_len, recent, budget in ((50, 3, 5, 20), (4096, 7, 256, 1024), (10000, 11, 1000, 2000),
+                                     (65536, 100, 64, 512), (1, 1, 1, 0), (1, 1, 0, 1), (8, 2, 4, 4)):
+        progress(f"roco_select ties n={n}")
+        s1 = rng.integers(0, 5, size=(3, n)).astype(np.float32)
+        s2 = rng.integers(0, 8, size=(3, n)).astype(np.float32) / 2.0
+        got = A.roco_select(torch.from_numpy(s1).to(gpu), torch.from_numpy(s2).to(gpu), q_len, recent, budget)
+        np.testing.assert_array_equal(got.cpu().numpy(), osel.roco_select(s1, s2, q_len, recent, budget),
+                                      err_msg=f"n={n} q_len={q_len} recent={recent} budget={budget}")
+    # nothing to select: an empty result, no launch
+    s = torch.zeros(2, 10, device=gpu)
+    assert A.roco_select(s, s, 10, 0, 0).shape == (2, 0)
 
 
 @pytest.mark.parametrize("case_cls,kw,dtype,q_len,kv_len", [

@@ -289,6 +289,99 @@ def test_topk_selection():
         np.testing.assert_array_equal(osel.topk_indices(row[None], k)[0], brute.topk_indices(row.tolist(), k))
 
 
+def test_topk_direction_and_nan_order():
+    # both directions against the exhaustive ranking, on rows full of ties, signed zeros, infinities and NaNs
+    rng = np.random.default_rng(1)
+    pool = np.array([0.0, -0.0, 1.0, -1.0, 2.5, np.inf, -np.inf, np.nan, -np.nan], dtype=np.float32)
+    for _ in range(40):
+        row = rng.choice(pool, size=30)
+        k = int(rng.integers(1, 31))
+        for largest in (True, False):
+            np.testing.assert_array_equal(osel.topk_indices(row[None], k, largest)[0],
+                                          brute.topk_indices(row.tolist(), k, largest))
+    # torch.topk (the library routine the reference calls) on distinct values with one NaN: the same sets
+    for seed in range(5):
+        x = torch.randperm(200, generator=torch.Generator().manual_seed(seed)).float() - 100.0
+        x[seed * 7] = float("nan")
+        for largest in (True, False):
+            for k in (1, 13, 199):
+                ref = torch.topk(x, k, largest=largest)[1].sort()[0].numpy()
+                np.testing.assert_array_equal(osel.topk_indices(x.numpy()[None], k, largest)[0], ref)
+
+
+def _roco_reference_torch(s1, s2, q_len, recent, budget):
+    """models/roco.py:54-61 as the reference writes it, in torch on the CPU."""
+    std = torch.sqrt(s2 / q_len - (s1 / q_len) ** 2)
+    kv_len = s1.shape[-1]
+    _, other = torch.topk(std, largest=False, k=kv_len - recent, dim=-1)
+    _, rec = torch.topk(std, largest=True, k=recent, dim=-1)
+    _, pick = torch.topk(s1.gather(dim=-1, index=other) / q_len, dim=-1, k=budget)
+    sel = torch.cat([other.gather(dim=-1, index=pick), rec], dim=-1)
+    return sel.sort(dim=-1)[0]
+
+
+def _roco_separated(seed, rows, n, q_len):
+    """Column sums whose std and mean values lie far apart (no two within many ulps): any correct rounding of the
+    reference's arithmetic orders them the same way."""
+    g = torch.Generator().manual_seed(seed)
+    mean = (torch.stack([torch.randperm(n, generator=g) for _ in range(rows)]).double() + 1.0) / (4.0 * n)
+    std = (torch.stack([torch.randperm(n, generator=g) for _ in range(rows)]).double() + 1.0) / (8.0 * n)
+    s1 = (mean * q_len).float()
+    s2 = ((std ** 2 + mean ** 2) * q_len).float()
+    return s1, s2
+
+
+def test_roco_select_matches_reference_lines():
+    for seed, (rows, n, q_len, recent, budget) in enumerate([(3, 64, 64, 8, 16), (2, 300, 300, 30, 100),
+                                                             (4, 97, 50, 0, 40), (2, 50, 50, 50, 0),
+                                                             (1, 128, 128, 1, 127)]):
+        s1, s2 = _roco_separated(seed, rows, n, q_len)
+        ref = _roco_reference_torch(s1, s2, q_len, recent, budget).numpy()
+        got = osel.roco_select(s1.numpy(), s2.numpy(), q_len, recent, budget)
+        np.testing.assert_array_equal(got, ref)
+        # planted mistakes: the largest std as `other`, or the pick by the smallest column sums
+        std = np.sqrt(s2.numpy() / q_len - (s1.numpy() / q_len) ** 2)
+        if 0 < budget < n - recent:
+            if recent > 0:
+                wrong_other = osel.topk_indices(std, n - recent, largest=True)
+                pick = osel.topk_indices(np.take_along_axis(s1.numpy(), wrong_other, -1), budget)
+                wrong = np.sort(np.concatenate([np.take_along_axis(wrong_other, pick, -1),
+                                                osel.topk_indices(std, recent)], -1), -1)
+                assert not np.array_equal(wrong, ref)
+            other = osel.topk_indices(std, n - recent, largest=False)
+            pick = osel.topk_indices(np.take_along_axis(s1.numpy(), other, -1), budget, largest=False)
+            wrong = np.sort(np.concatenate([np.take_along_axis(other, pick, -1), osel.topk_indices(std, recent)], -1), -1)
+            assert not np.array_equal(wrong, ref)
+
+
+def test_roco_select_ties_nan_and_invariants():
+    rng = np.random.default_rng(3)
+    for _ in range(30):
+        n = int(rng.integers(2, 24))
+        recent = int(rng.integers(0, n + 1))
+        budget = int(rng.integers(0, n - recent + 1))
+        s1 = rng.integers(0, 4, size=n).astype(np.float32)
+        s2 = rng.integers(0, 6, size=n).astype(np.float32)  # s2 < s1**2 / q_len somewhere: NaN std
+        q_len = int(rng.integers(1, 5))
+        got = osel.roco_select(s1[None], s2[None], q_len, recent, budget)[0]
+        # exhaustive-ranking restatement of roco.py:54-61 (float32 arithmetic, torch's GPU rounding of / q_len)
+        rcp = np.float32(1) / np.float32(q_len)
+        with np.errstate(invalid="ignore"):
+            std = [float(np.sqrt(np.float32(b) * rcp - (np.float32(a) * rcp) * (np.float32(a) * rcp)))
+                   for a, b in zip(s1, s2)]
+        other = brute.topk_indices(std, n - recent, largest=False)
+        rec = brute.topk_indices(std, recent, largest=True)
+        pick = brute.topk_indices([float(np.float32(s1[i]) * rcp) for i in other], budget)
+        want = sorted([other[p] for p in pick] + rec)
+        np.testing.assert_array_equal(got, want)
+        assert len(got) == budget + recent and np.all(np.diff(got) >= 0)
+    # recent = 0 keeps the budget largest column sums (H2O's rule); budget = 0 keeps the largest std
+    s1, s2 = _roco_separated(9, 2, 80, 80)
+    np.testing.assert_array_equal(osel.roco_select(s1.numpy(), s2.numpy(), 80, 0, 20), osel.topk_indices(s1.numpy(), 20))
+    std = np.sqrt(s2.numpy() / np.float32(80) - (s1.numpy() / np.float32(80)) ** 2)
+    np.testing.assert_array_equal(osel.roco_select(s1.numpy(), s2.numpy(), 80, 10, 0), osel.topk_indices(std, 10))
+
+
 def _sel_inputs(seed, B=1, S=20, H=2, D=8, Sk=None, scale=2.0):
     g = torch.Generator().manual_seed(seed)
     Sk = S if Sk is None else Sk

@@ -134,9 +134,12 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool
 
 def attention_colsum(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor, *, causal: bool = True,
                      softcap: float = 0.0, window: int = 0, scale: float | None = None,
-                     ref_rounding: bool = False, lse_base2: bool = False) -> torch.Tensor:
+                     ref_rounding: bool = True, lse_base2: bool = False) -> torch.Tensor:
     """Column sums of the softmax probabilities over the query axis, per query head: [B, Hq, Sk] fp32, recomputed
-    from q, k and the lse written by attention(..., return_lse=True) with the same options (lse_base2 included)."""
+    from q, k and the lse written by attention(..., return_lse=True) with the same options (ref_rounding and
+    lse_base2 included). ref_rounding (the default) rounds the 16-bit scores where the reference's eager module
+    rounds them (attn.py:29, gemma2.py:29-33), which the selection cases' 1e-3 contract on the sums needs;
+    ref_rounding=False keeps fp32 scores (faster, but up to ~1% off the reference's sums in 16-bit)."""
     dev = _lib.require_gpu(q, k, lse)
     _check_qk("attention_colsum", q, k)
     B, Sq, Hq, D = q.shape
@@ -169,8 +172,9 @@ def h2o_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, ref_roun
 
 def attention_colscore(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor, *, epilogue: int,
                        thr: torch.Tensor | None = None, causal: bool = True, window: int = 0,
-                       scale: float | None = None, ref_rounding: bool = False, lse_base2: bool = False):
-    """Column scores over the query axis from q, k and the forward's lse (same options), per query head [B, Hq, Sk]:
+                       scale: float | None = None, ref_rounding: bool = True, lse_base2: bool = False):
+    """Column scores over the query axis from q, k and the forward's lse (same options, ref_rounding included: see
+    attention_colsum), per query head [B, Hq, Sk]:
     epilogue COL_SUM -> sum_i p; COL_SUM_SQ -> (sum_i p, sum_i p^2) (roco.py:43-47); COL_ANY_GE -> bool
     any_i p[i, j] >= thr[i, j] with thr fp32 [Sq, Sk] (corm.py:35-37)."""
     dev = _lib.require_gpu(q, k, lse, thr)

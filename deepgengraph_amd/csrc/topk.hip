@@ -66,20 +66,28 @@ __device__ uint64_t radix_take(const uint32_t (&key)[PER], uint64_t cand, uint32
   for (int shift = 24; shift >= 0; shift -= 8) {
     for (int i = tid; i < kTopkWaves * 256; i += kTopkThreads) (&sh.hist[0][0])[i] = 0u;
     __syncthreads();
+    if (shift == 24) {
+      // The top byte (sign and leading exponent bits) of one row's scores is nearly constant, so most lanes of a
+      // wave hit the same bin and their LDS atomics would serialise on one address: the lanes whose digit equals
+      // the first active lane's add as one. The lower bytes spread over the bins, where this costs more than it
+      // saves.
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      // Scores of one row share their leading bits, so most lanes of a wave hit the same bin and their LDS atomics
-      // would serialise on one address: the lanes whose digit equals the first active lane's add as one.
-      const bool act = ((cand >> j) & 1) && (key[j] & pmask) == prefix;
-      const uint32_t d = (key[j] >> shift) & 255u;
-      const uint64_t active = __ballot(act);
-      if (active) {
-        const int leader = __ffsll((long long)active) - 1;
-        const uint32_t d0 = __shfl(d, leader, 64);
-        const uint64_t same = __ballot(act && d == d0);
-        if (lane == leader) atomicAdd(&sh.hist[wv][d0], (uint32_t)__popcll(same));
-        else if (act && d != d0) atomicAdd(&sh.hist[wv][d], 1u);
+      for (int j = 0; j < PER; ++j) {
+        const bool act = (cand >> j) & 1;
+        const uint32_t d = key[j] >> 24;
+        const uint64_t active = __ballot(act);
+        if (active) {
+          const int leader = __ffsll((long long)active) - 1;
+          const uint32_t d0 = __shfl(d, leader, 64);
+          const uint64_t same = __ballot(act && d == d0);
+          if (lane == leader) atomicAdd(&sh.hist[wv][d0], (uint32_t)__popcll(same));
+          else if (act && d != d0) atomicAdd(&sh.hist[wv][d], 1u);
+        }
       }
+    } else {
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (((cand >> j) & 1) && (key[j] & pmask) == prefix) atomicAdd(&sh.hist[wv][(key[j] >> shift) & 255u], 1u);
     }
     __syncthreads();
     // Thread t < 256 takes bin 255 - t: an inclusive scan over t counts the candidates in bins >= 255 - t.

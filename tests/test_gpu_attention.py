@@ -290,6 +290,25 @@ def test_h2o_matches_oracle(gpu, S, H, D, sinks, dtype):
     np.testing.assert_array_equal(A.topk_indices(ref_cs.to(gpu), kk).cpu().numpy(), osel.topk_indices(ref_cs.numpy(), kk))
 
 
+def _colsum_reference(q, k, causal, softcap, window):
+    """Column sums of the reference's probabilities (scores rounded in the input dtype as attn.py:29 and
+    gemma2.py:29-33 round them, fp32 softmax, masked pairs -inf, rows that see no key contributing nothing), per
+    query head, summed in float64. GQA: query head h reads KV head h // (Hq / Hkv)."""
+    B, Sq, Hq, D = q.shape
+    Sk, Hkv = k.shape[1], k.shape[2]
+    qt = q.transpose(1, 2)
+    kT = k.transpose(1, 2).repeat_interleave(Hq // Hkv, 1).transpose(-2, -1)
+    total = torch.zeros(B, Hq, Sk, dtype=torch.float64)
+    for i0 in range(0, Sq, 256):
+        n = min(256, Sq - i0)
+        s = oa._scores(qt[:, :, i0:i0 + n], kT, D, softcap or None).float()
+        m = oa._mask(i0, n, Sq, Sk, causal, window or None)
+        if m is not None:
+            s = s.masked_fill(m, float("-inf"))
+        total += torch.softmax(s, -1).nan_to_num(0.0).double().sum(2)
+    return total
+
+
 @pytest.mark.parametrize("D,Sq,Sk,causal,window,softcap,dtype,base2", [
     (64, 200, 200, True, 50, 20.0, torch.bfloat16, False),
     (128, 200, 200, True, 50, 20.0, torch.bfloat16, False),
@@ -298,29 +317,22 @@ def test_h2o_matches_oracle(gpu, S, H, D, sinks, dtype):
     (128, 300, 300, False, 0, 0.0, torch.float16, True),
     (128, 640, 640, True, 100, 0.0, torch.float16, True),
     (256, 160, 160, True, 0, 30.0, torch.bfloat16, False),
+    (256, 300, 300, True, 64, 50.0, torch.float16, True),
 ])
 def test_colsum_variants(gpu, D, Sq, Sk, causal, window, softcap, dtype, base2):
-    # column sums (soft-cap, window, GQA, Sq != Sk, both lse forms) against sums of fp32 softmax probabilities
+    # column sums (soft-cap, window, GQA, Sq != Sk, both lse forms) with the default reference rounding against the
+    # reference's probabilities at the column-sum contract (1e-3 rel); the fp32-score opt-out against fp32 sums
     B, Hq, Hkv = 1, 4, 2
     q, k, v = _qkv(B, Sq, Sk, Hq, Hkv, D, dtype, 77 + D + Sq)
     kw = dict(causal=causal, softcap=softcap, window=window, lse_base2=base2)
-    out, lse = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), return_lse=True, **kw)
-    cs = A.attention_colsum(q.to(gpu), k.to(gpu), lse, **kw).cpu()
-    qt, kt = q.transpose(1, 2).float(), k.transpose(1, 2).repeat_interleave(Hq // Hkv, 1).float()
-    s = torch.matmul(qt, kt.transpose(-1, -2)) / math.sqrt(D)
-    if softcap:
-        s = softcap * torch.tanh(s / softcap)
-    i = torch.arange(Sq).view(Sq, 1) + (Sk - Sq)
-    j = torch.arange(Sk).view(1, Sk)
-    hidden = torch.zeros(Sq, Sk, dtype=torch.bool)
-    if causal:
-        hidden |= j > i
-    if window:
-        hidden |= i - j >= window
-    s = s.masked_fill(hidden, float("-inf"))
-    ref = torch.softmax(s, -1).nan_to_num(0.0).sum(2)   # rows that see no key contribute nothing
     what = f"colsum D{D} Sq{Sq} Sk{Sk} causal{causal} w{window} sc{softcap} {dtype} base2={base2}"
-    assert_close(cs, ref, 1e-3, 1e-2, what + " (kernel keeps fp32 scores, reference fp32)")
+    _, lse = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), return_lse=True, ref_rounding=True, **kw)
+    cs = A.attention_colsum(q.to(gpu), k.to(gpu), lse, **kw).cpu()
+    _colsum_check(cs, _colsum_reference(q, k, causal, softcap, window).float(), what + " reference rounding")
+    _, lse = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), return_lse=True, ref_rounding=False, **kw)
+    cs = A.attention_colsum(q.to(gpu), k.to(gpu), lse, ref_rounding=False, **kw).cpu()
+    ref = _colsum_reference(q.float(), k.float(), causal, softcap, window).float()
+    assert_close(cs, ref, 1e-3, 1e-2, what + " fp32 scores vs fp32 reference")
 
 
 def test_column_wrappers_reject_mismatched_k(gpu):

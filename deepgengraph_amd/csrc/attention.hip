@@ -1016,6 +1016,7 @@ __global__ void __launch_bounds__(kThreads) attn_colsum_kernel(AttnParams p) {
           pe = kf_prob(x * c, erp[(int64_t)min(qg, p.Sq - 1) * p.er_ss + kjc], Ls[buf][row], p);
         else
           pe = fast_exp2(fmaf(x, c, -Ls[buf][row]));
+        bool vis = true;  // (qg, kj) a visible pair of an existing row and key
         if (need_mask) {
           bool ok = qg < p.Sq && kj < p.Sk;
           if constexpr (MASK) {
@@ -1024,8 +1025,10 @@ __global__ void __launch_bounds__(kThreads) attn_colsum_kernel(AttnParams p) {
             if (p.window > 0) ok = ok && rel < p.window;
           }
           pe = ok ? pe : 0.f;
+          vis = ok;
         }
-        acc.add(pe, qg < p.Sq, min(qg, p.Sq - 1), kjc, p);
+        // Corm compares visible pairs here; the masked ones (p = 0) are ORed in by corm_masked_or_kernel
+        acc.add(pe, EPI == kColAnyGe ? vis : qg < p.Sq, min(qg, p.Sq - 1), kjc, p);
       }
     }
 
@@ -1124,6 +1127,7 @@ attn_colsum_d128_kernel(AttnParams p) {
   }
   if (t_full1 * BQ > p.Sq) t_full1 = p.Sq / BQ;  // ragged last tile
   if (EPI == kColKF && !p.er_lane32) t_full1 = t_full0;  // exp_rand offsets too wide for the full-tile loads
+  if (EPI == kColAnyGe && !p.thr_lane32) t_full1 = t_full0;  // threshold offsets too wide for the full-tile loads
   if (t_full1 < t_full0) t_full1 = t_full0;
 
   // Direct-load lane constants (as the forward's K tiles).
@@ -1169,6 +1173,8 @@ attn_colsum_d128_kernel(AttnParams p) {
   // KeyFormer exp_rand of (row, kjc) for tiles whose rows all exist: a wave-uniform tile address (scalar registers)
   // plus a 32-bit offset, this lane's part (rows 4g apart, column kjc) plus the row's, one add per load.
   const uint32_t er_lane_b = EPI == kColKF ? (uint32_t)((4 * g * p.er_ss + kjc) * 4) : 0u;
+  // Corm's thresholds of (row, kjc), addressed the same way.
+  const uint32_t thr_lane_b = EPI == kColAnyGe ? (uint32_t)((4 * g * p.thr_rs + kjc) * 4) : 0u;
 
   auto tile = [&](const int t, auto masked) {
     const uint32_t st = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B);
@@ -1191,6 +1197,29 @@ attn_colsum_d128_kernel(AttnParams p) {
 #pragma unroll
           for (int j = 0; j < 16; ++j)
             ev[mb][j] = erp[(int64_t)min(t * BQ + 4 * g + 32 * mb + 8 * (j >> 2) + (j & 3), p.Sq - 1) * p.er_ss + kjc];
+      }
+    }
+    // Corm: the tile's thresholds for this lane's key, requested before the QK^T MFMAs so that the loads overlap
+    // them (corm.py:35-37 compares each p with thr[i][j])
+    float tv[NMB][16];
+    if constexpr (EPI == kColAnyGe) {
+      if constexpr (!decltype(masked)::value) {  // every row of the tile exists (and thr_lane32 holds)
+        const char* rb = reinterpret_cast<const char*>(p.thr + (int64_t)(t * BQ) * p.thr_rs);
+        uint32_t ss_b = (uint32_t)(p.thr_rs * 4);
+        asm volatile("" : "+s"(ss_b));  // per tile: keeps the 64 offsets from being hoisted into registers
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const uint32_t row_b = (uint32_t)(32 * mb + 8 * (j >> 2) + (j & 3)) * ss_b;
+            tv[mb][j] = *reinterpret_cast<const float*>(rb + (thr_lane_b + row_b));
+          }
+      } else {  // rows past the end read the last row (they take no part)
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            tv[mb][j] = p.thr[(int64_t)min(t * BQ + 4 * g + 32 * mb + 8 * (j >> 2) + (j & 3), p.Sq - 1) * p.thr_rs + kjc];
       }
     }
     f32x16 sacc[NMB];
@@ -1229,7 +1258,7 @@ attn_colsum_d128_kernel(AttnParams p) {
           pe = kf_prob(x * c, ev[mb][j], l2, p);
         else
           pe = fast_exp2(fmaf(x, c, -l2));
-        bool valid = true;
+        bool valid = true, vis = true;
         if constexpr (decltype(masked)::value) {
           valid = o < rows_left;
           bool ok = valid;
@@ -1238,8 +1267,11 @@ attn_colsum_d128_kernel(AttnParams p) {
             if (p.window > 0) ok = ok && rel0 + o < p.window;
           }
           pe = ok ? pe : 0.f;
+          vis = ok;
         }
-        acc.add(pe, valid, min(t * BQ + 4 * g + o, p.Sq - 1), kjc, p);
+        // Corm compares visible pairs here; the masked ones (p = 0) are ORed in by corm_masked_or_kernel
+        if constexpr (EPI == kColAnyGe) acc.any |= vis && pe >= tv[mb][j];
+        else acc.add(pe, valid, min(t * BQ + 4 * g + o, p.Sq - 1), kjc, p);
       }
     }
   };
@@ -1247,7 +1279,9 @@ attn_colsum_d128_kernel(AttnParams p) {
 #pragma unroll
   for (int i = 0; i < NSTAGE - 1; ++i)
     if (t_begin + i < t_end) issue(t_begin + i);
-  auto step = [&](const int t, auto masked) {
+  // Corm: whether this wave's keys are all decided (no tile of its range left, or every key flagged).
+  bool wave_done = wt_begin >= wt_end;
+  auto step = [&](const int t, auto masked) -> bool {
     // Tiles t+1 .. t+after may stay in flight; the last wave issues NLSE more copies per tile.
     const int after = min(NSTAGE - 2, t_end - 1 - t);
     if (w == NW - 1) {
@@ -1259,13 +1293,30 @@ attn_colsum_d128_kernel(AttnParams p) {
       else if (NSTAGE >= 3 && after >= 1) wait_vmem<GPW>();
       else wait_vmem<0>();
     }
-    __syncthreads();
+    if constexpr (EPI == kColAnyGe) {
+      // Corm ORs over the query rows: once every key of every wave is flagged, no later tile can change the
+      // result, and the workgroup stops. The vote doubles as the tile's barrier; the copies of this tile have
+      // landed and none is in flight yet (NSTAGE 2), so nothing still writes into the LDS when it stops.
+      static_assert(EPI != kColAnyGe || NSTAGE == 2, "the early stop assumes no copy in flight at the barrier");
+      if (__syncthreads_and(wave_done)) return false;
+    } else {
+      __syncthreads();
+    }
     if (t + NSTAGE - 1 < t_end) issue(t + NSTAGE - 1);
-    if (t >= wt_begin && t < wt_end) tile(t, masked);
+    if (t >= wt_begin && t < wt_end) {
+      tile(t, masked);
+      if constexpr (EPI == kColAnyGe) {
+        // this lane's key is decided when either half of its rows flagged it (keys past the end count as decided)
+        const bool decided = (acc.any | __shfl_xor(acc.any, 32, 64)) != 0 || kj >= p.Sk;
+        wave_done = t + 1 >= wt_end || __all(decided);
+      }
+    }
+    return true;
   };
-  for (int t = t_begin; t < t_full0; ++t) step(t, std::true_type{});
-  for (int t = t_full0; t < t_full1; ++t) step(t, std::false_type{});
-  for (int t = t_full1; t < t_end; ++t) step(t, std::true_type{});
+  bool go = true;
+  for (int t = t_begin; go && t < t_full0; ++t) go = step(t, std::true_type{});
+  for (int t = t_full0; go && t < t_full1; ++t) go = step(t, std::false_type{});
+  for (int t = t_full1; go && t < t_end; ++t) go = step(t, std::true_type{});
 
   acc.store(p, bh, kj, g);
 }
@@ -1552,6 +1603,38 @@ extern "C" int dgg_attn_prefill_rope(const void* q, const void* k, const void* v
 }
 
 namespace {
+// Corm over the masked pairs (corm.py:35-37 compares every query row, masked pairs included): a masked pair of a
+// row that sees at least one key has p = 0 (softmax of -inf), so it flags its key when thr[i][j] <= 0; a row that
+// sees no key at all has NaN probabilities (0 / 0) and flags nothing. The column kernels compare the visible pairs
+// only; this kernel, run after them on the same stream, sets any_out[bh][j] = 1 for every (batch, head) when some
+// masked pair of a non-empty row has thr[i][j] <= 0 (the thresholds are shared by all heads). One thread per key and
+// chunk of kMaskedRows rows, reading only the masked part of the chunk: for causal the rows before the key's
+// diagonal, for a window the rows past its end. Flags are written only when found, as plain byte stores of 1.
+constexpr int kMaskedRows = 64;
+__global__ void __launch_bounds__(256) corm_masked_or_kernel(const float* __restrict__ thr, int64_t rs, int Sq, int Sk,
+                                                             int offset, int causal, int window, uint8_t* any_out,
+                                                             int64_t nbh) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= Sk) return;
+  const int r0 = blockIdx.y * kMaskedRows, r1 = min(Sq, r0 + kMaskedRows);
+  // masked rows of key j: [a0, a1) before the diagonal (rows i + offset < j that see a key: i + offset >= 0),
+  // [b0, r1) past the window (i + offset - j >= window)
+  int a0 = r1, a1 = r1, b0 = r1;
+  const int64_t diag = (int64_t)j - offset;  // first row that sees key j (causal)
+  if (causal) {
+    a0 = (int)max<int64_t>(r0, max<int64_t>(0, -(int64_t)offset));
+    a1 = (int)min<int64_t>(r1, diag);
+  }
+  if (window > 0) b0 = (int)min<int64_t>(r1, max<int64_t>(r0, diag + window));  // never overlaps [a0, a1)
+  bool hit = false;
+#pragma unroll 8
+  for (int i = a0; i < a1; ++i) hit |= thr[(int64_t)i * rs + j] <= 0.f;
+#pragma unroll 8
+  for (int i = b0; i < r1; ++i) hit |= thr[(int64_t)i * rs + j] <= 0.f;
+  if (hit)
+    for (int64_t bh = 0; bh < nbh; ++bh) any_out[bh * Sk + j] = 1;
+}
+
 // Shared body of dgg_attn_colsum and dgg_attn_colscore.
 int colscore(const char* op, const void* q, const void* k, const float* lse, int epi, float* out0, float* out1,
              uint8_t* out_any, const float* thr, int64_t thr_row_stride, int64_t B, int64_t Sq, int64_t Sk, int64_t Hq,
@@ -1578,25 +1661,31 @@ int colscore(const char* op, const void* q, const void* k, const float* lse, int
   p.any_out = out_any;
   p.thr = thr;
   p.thr_rs = thr_row_stride;
+  p.thr_lane32 = (132 * thr_row_stride + Sk) * 4 < (1ll << 31) ? 1 : 0;
   p.q_sb = strides[0]; p.q_ss = strides[1]; p.q_sh = strides[2];
   p.k_sb = strides[3]; p.k_ss = strides[4]; p.k_sh = strides[5];
   hipStream_t st = dgg::as_stream(stream);
   if (dtype == DGG_F32) {
     p.n_tiles = (int)((Sk + f32_rows_per_tile() - 1) / f32_rows_per_tile());
     launch_attn_f32_col(p, (int)D, epi, st);
-    return dgg::check_launch(op);
-  }
-  const int64_t bk = D == 128 ? kC128BK : kCBK;
-  p.n_tiles = (int)((Sk + bk - 1) / bk);
-  const bool ref = (flags & DGG_ATTN_REF_ROUNDING) != 0;
-  if (dtype == DGG_BF16) {
-    if (D == 64) pick_col<BF16, 64>(p, ref, epi, st);
-    else if (D == 128) pick_col<BF16, 128>(p, ref, epi, st);
-    else pick_col<BF16, 256>(p, ref, epi, st);
   } else {
-    if (D == 64) pick_col<F16, 64>(p, ref, epi, st);
-    else if (D == 128) pick_col<F16, 128>(p, ref, epi, st);
-    else pick_col<F16, 256>(p, ref, epi, st);
+    const int64_t bk = D == 128 ? kC128BK : kCBK;
+    p.n_tiles = (int)((Sk + bk - 1) / bk);
+    const bool ref = (flags & DGG_ATTN_REF_ROUNDING) != 0;
+    if (dtype == DGG_BF16) {
+      if (D == 64) pick_col<BF16, 64>(p, ref, epi, st);
+      else if (D == 128) pick_col<BF16, 128>(p, ref, epi, st);
+      else pick_col<BF16, 256>(p, ref, epi, st);
+    } else {
+      if (D == 64) pick_col<F16, 64>(p, ref, epi, st);
+      else if (D == 128) pick_col<F16, 128>(p, ref, epi, st);
+      else pick_col<F16, 256>(p, ref, epi, st);
+    }
+  }
+  if (epi == kColAnyGe && Sq > 0 && (p.causal || p.window > 0)) {
+    const dim3 grid((unsigned)((Sk + 255) / 256), (unsigned)((Sq + kMaskedRows - 1) / kMaskedRows));
+    hipLaunchKernelGGL(corm_masked_or_kernel, grid, dim3(256), 0, st, thr, thr_row_stride, (int)Sq, (int)Sk, p.offset,
+                       p.causal, p.window, out_any, B * Hq);
   }
   return dgg::check_launch(op);
 }

@@ -31,6 +31,7 @@ struct AttnParams {
   int64_t er_sb, er_sh, er_ss;
   float kf_inv_tau;      // 1 / tau of the perturbed softmax
   int er_lane32;         // (132 * er_ss + Sk) * 4 < 2^31: the exp_rand byte offsets within a tile fit 32 bits
+  int thr_lane32;        // (132 * thr_rs + Sk) * 4 < 2^31: the threshold byte offsets within a tile fit 32 bits
   int64_t q_sb, q_ss, q_sh;
   int64_t k_sb, k_ss, k_sh;
   int64_t v_sb, v_ss, v_sh;

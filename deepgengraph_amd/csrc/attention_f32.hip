@@ -192,7 +192,7 @@ __global__ void __launch_bounds__(kThr) attn_col_f32_kernel(AttnParams p) {
       if (p.window > 0) ok = ok && qg + p.offset - kj < p.window;
       const float pe = ok ? expf(x - Ls[i]) : 0.f;
       if constexpr (EPI == kColAnyGe) {
-        if (qg < p.Sq && kj < p.Sk) any |= pe >= p.thr[(int64_t)qg * p.thr_rs + kj];
+        if (ok) any |= pe >= p.thr[(int64_t)qg * p.thr_rs + kj];  // masked pairs: corm_masked_or_kernel
       } else {
         sum += pe;
         if constexpr (EPI == kColSumSq) sum2 = fmaf(pe, pe, sum2);

@@ -135,8 +135,12 @@ int dgg_attn_colsum(const void* q, const void* k, const float* lse, float* colsu
  *   DGG_COL_SUM_SQ: out0 = sum_i p, out1 = sum_i p^2                (RoCo roco.py:43-47)
  *   DGG_COL_ANY_GE: out_any[b,h,j] = any_i (p[b,h,i,j] >= thr[i*thr_row_stride + j]), uint8 0/1
  *                                                                   (Corm corm.py:35-37; thr = corm_mask [Sq, Sk])
- * Rows i >= Sq take no part; masked pairs have p = 0 (as the reference's softmax of -inf). The two new
- * epilogues take no soft-cap (DGG_ERR_UNSUPPORTED). Other arguments as dgg_attn_colsum. */
+ * Rows i >= Sq take no part. As in the reference, every query row is compared: a masked pair of a row that sees
+ * at least one key has p = 0 (softmax of -inf), so it flags its key when thr <= 0; a row that sees no key at all
+ * (Sq > Sk, causal) has NaN probabilities and flags nothing. DGG_COL_ANY_GE launches a second small kernel for the
+ * masked pairs (it reads the masked part of thr once for all heads), and at head_dim 128 the column pass stops a
+ * workgroup once all of its keys are flagged (an OR cannot change after that). The two new epilogues take no
+ * soft-cap (DGG_ERR_UNSUPPORTED). Other arguments as dgg_attn_colsum. */
 #define DGG_COL_SUM 0
 #define DGG_COL_SUM_SQ 1
 #define DGG_COL_ANY_GE 2

@@ -5,6 +5,7 @@ import pytest
 import torch
 
 from conftest import assert_close, progress
+from deepgengraph_amd import _lib
 from deepgengraph_amd import attention as A
 from deepgengraph_amd.compile import compile as dgg_compile
 from oracle import attention as oa
@@ -117,6 +118,91 @@ def test_keyformer_wide_exp_rand_rows(gpu):
     assert_close(out.cpu().float(), ref_out.float(), *TOL_F16, "keyformer wide out")
     assert_close(score.cpu(), ref_score, 1e-6, 1e-3, "keyformer wide kf_score")
     del buf
+
+
+@pytest.mark.parametrize("kind", ["never", "some_keys", "late_rows", "zero", "nan_inf"])
+def test_corm_thresholds_that_decide_late_or_never(gpu, kind):
+    # The head_dim-128 Corm column pass stops a workgroup once every key of every wave is flagged. These
+    # thresholds keep keys undecided for the whole pass (never: p <= 1 < 2), for some key ranges only, until the
+    # last rows, or decide them at once (zero); NaN never selects, -inf always does.
+    S, H, D = 1100, 2, 128
+    q, k, v = _qkv(S, H, D, 5 * S + len(kind), sinks=4)
+    g = torch.Generator().manual_seed(17)
+    thr = oa.corm_mask(S, S).clone()
+    if kind == "never":
+        thr.fill_(2.0)
+    elif kind == "some_keys":
+        thr[:, 300:700] = 2.0  # keys of these columns never pass; the others decide as usual
+    elif kind == "late_rows":
+        thr[: S - 40] = 2.0    # only the last 40 rows can flag anything
+    elif kind == "zero":
+        thr.zero_()            # p >= 0 everywhere, masked pairs included
+    else:
+        thr = torch.rand(S, S, generator=g)
+        thr[torch.rand(S, S, generator=g) < 0.3] = float("nan")
+        thr[torch.rand(S, S, generator=g) < 0.01] = float("-inf")
+    progress(f"corm thresholds {kind}")
+    _, hit = A.corm_attention(q.to(gpu), k.to(gpu), v.to(gpu), thr.to(gpu))
+    n = _corm_check(hit, q, k, v, thr, f"corm thresholds {kind}")
+    if kind == "never":
+        assert not hit.any()
+    if kind == "zero":
+        assert hit.all()
+    if kind == "some_keys":
+        assert not hit[..., 300:700].any() and n == 0
+
+
+def _corm_reference(q, k, thr, causal, window):
+    """corm.py:35-37 over every query row: probs >= thr with the reference's probabilities (scores rounded in the
+    input dtype, masked pairs -inf, so p = 0 there and NaN on rows that see no key), any over the rows. Also
+    returns the float64 probabilities for the tie check."""
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    s = oa._scores(q.transpose(1, 2), k.transpose(1, 2).transpose(-2, -1), D).float()
+    m = oa._mask(0, Sq, Sq, Sk, causal, window or None)
+    if m is not None:
+        s = s.masked_fill(m, float("-inf"))
+    probs = torch.softmax(s, -1)
+    return (probs >= thr).any(dim=2), probs.double()
+
+
+@pytest.mark.parametrize("D,dtype,Sq,Sk,causal,window", [
+    (128, torch.float16, 600, 600, True, 0),
+    (128, torch.float16, 700, 400, True, 0),      # Sq > Sk: the first 300 rows see no key (NaN probabilities)
+    (128, torch.bfloat16, 500, 500, True, 97),    # causal + window: masked pairs on both sides
+    (128, torch.float16, 300, 450, False, 80),    # window without causal
+    (64, torch.float16, 400, 300, True, 0),       # the generic column kernel
+    (256, torch.bfloat16, 300, 300, True, 50),
+    (128, torch.float32, 300, 200, True, 0),      # the fp32 column kernel
+])
+def test_corm_masked_pairs_and_empty_rows(gpu, D, dtype, Sq, Sk, causal, window):
+    # thresholds 2 (never passed) except: <= 0 at random masked pairs, and at every pair of the rows that see
+    # no key; plus random positive thresholds on a band so that visible pairs flag some keys too
+    g = torch.Generator().manual_seed(D + Sq + Sk + window)
+    q = torch.randn(1, Sq, 2, D, generator=g).to(dtype)
+    k = torch.randn(1, Sk, 2, D, generator=g).to(dtype)
+    v = torch.randn(1, Sk, 2, D, generator=g).to(dtype)
+    thr = torch.full((Sq, Sk), 2.0)
+    hidden = oa._mask(0, Sq, Sq, Sk, causal, window or None)
+    pick = torch.rand(Sq, Sk, generator=g) < 0.002
+    thr[hidden & pick] = torch.tensor([0.0, -0.0, -1.0, float("-inf")])[torch.randint(0, 4, (int((hidden & pick).sum()),),
+                                                                                      generator=g)]
+    if Sq > Sk and causal:
+        thr[: Sq - Sk] = -1.0  # rows that see no key: NaN >= -1 is False, they flag nothing
+    band = torch.rand(Sq, Sk, generator=g) < 0.05
+    thr[band & ~hidden] = 0.02
+    progress(f"corm masked pairs D{D} {dtype} Sq{Sq} Sk{Sk} causal={causal} w={window}")
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    _, lse = A.attention(qg, kg, vg, causal=causal, window=window, return_lse=True, ref_rounding=True, lse_base2=True)
+    hit = A.attention_colscore(qg, kg, lse, epilogue=_lib.COL_ANY_GE, thr=thr.to(gpu), causal=causal, window=window,
+                               lse_base2=True).cpu()
+    ref, probs = _corm_reference(q, k, thr, causal, window)
+    diff = hit != ref
+    if diff.any():  # only a visible pair whose p ties its threshold to fp32 rounding may differ
+        b, h, j = diff.nonzero()[0].tolist()
+        col_p, col_t = probs[b, h, :, j], thr[:, j].double()
+        assert ((col_p - col_t).abs() / col_t.abs() < 2e-6).any(), f"key {j} head {h} differs away from a tie"
+    assert hit.any() and not hit.all()
 
 
 def test_colscore_thresholds_and_strides(gpu):

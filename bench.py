@@ -75,6 +75,28 @@ def _events_time(fn, iters: int, warmup: int) -> float:
     return ms
 
 
+def _variant(fn, iters: int, warm_ms: float = 60.0):
+    """A secondary workload's GPU time per call (ms) by _events_time, after a warm-up of about warm_ms of its own
+    work (at least 3 calls): each section first builds its inputs on the host, which leaves the GPU idle, and the
+    part lowers and then raises its clock over the first tens of milliseconds of load that follow. Returns
+    (ms, info) with the warm-up call count and the shader clock just before and after the timed calls."""
+    dev = torch.cuda.current_device()
+    clk = torch.zeros(2, 2, dtype=torch.int64, device=dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    fn()
+    torch.cuda.synchronize()
+    one_ms = (time.perf_counter() - t0) * 1e3
+    warm = int(min(2000, max(3, warm_ms / max(one_ms, 1e-3))))
+    for _ in range(warm):
+        fn()
+    _clock_probe(dev, clk, 0)
+    ms = _events_time(fn, iters, 0)
+    _clock_probe(dev, clk, 1)
+    torch.cuda.synchronize()
+    return ms, dict(warmup=warm + 1, clock_mhz=[_clock_mhz(clk, 0), _clock_mhz(clk, 1)])
+
+
 def _clock_probe(dev, buf, slot):
     """Enqueues the shader-clock probe (20 us spin) on the current stream; its result lands in buf[slot]."""
     from deepgengraph_amd import _lib
@@ -222,36 +244,36 @@ def bench_variants(args, dev):
     res = {}
     cfg = C.CFG3
     q, k, v, _ = C.attn_inputs(cfg, device=dev)
-    ms = _events_time(
-        lambda: A.attention(q, k, v, causal=True, softcap=cfg.softcap, window=cfg.window), 10, 3)
+    ms, info = _variant(lambda: A.attention(q, k, v, causal=True, softcap=cfg.softcap, window=cfg.window), 10)
     res["cfg3_gemma2"] = dict(ms=round(ms, 4), tflops=round(cfg.flops() / (ms * 1e-3) / 1e12, 1),
-                              frac=round(cfg.flops() / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))
+                              frac=round(cfg.flops() / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), **info)
     del q, k, v
     cfg = C.CFG4
     q, k, v, _ = C.attn_inputs(cfg, device=dev)
-    ms = _events_time(lambda: A.topk_indices(A.h2o_attention(q, k, v)[1], cfg.topk), 5, 1)
+    ms, info = _variant(lambda: A.topk_indices(A.h2o_attention(q, k, v)[1], cfg.topk), 5)
     res["cfg4_h2o_fwd_colsum_topk"] = dict(ms=round(ms, 4),
                                            tflops=round(cfg.reference_flops() / (ms * 1e-3) / 1e12, 1),
-                                           frac=round(cfg.reference_flops() / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))
+                                           frac=round(cfg.reference_flops() / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                                           **info)
     cs = A.h2o_attention(q, k, v)[1]
-    ms = _events_time(lambda: A.topk_indices(cs, cfg.topk), 20, 2)
-    ms_t = _events_time(lambda: torch.topk(cs, k=cfg.topk, dim=-1, sorted=True)[1].sort(dim=-1)[0], 20, 2)
-    res["cfg4_topk256"] = dict(us=round(ms * 1e3, 2), torch_us=round(ms_t * 1e3, 2))
+    ms, info = _variant(lambda: A.topk_indices(cs, cfg.topk), 20)
+    ms_t, _ = _variant(lambda: torch.topk(cs, k=cfg.topk, dim=-1, sorted=True)[1].sort(dim=-1)[0], 20)
+    res["cfg4_topk256"] = dict(us=round(ms * 1e3, 2), torch_us=round(ms_t * 1e3, 2), **info)
     del cs
     # the other selection cases of the reference at config-4 shapes (same inputs; Corm's threshold 1/(i+1))
     thr = torch.ones(cfg.Sq, cfg.Sk, device=dev) / torch.arange(1, cfg.Sq + 1, device=dev, dtype=torch.float32)[:, None]
     for name, fn in (("cfg4_roco", lambda: A.roco_attention(q, k, v)),
                      ("cfg4_snapkv", lambda: A.snapkv_attention(q, k, v)),
                      ("cfg4_corm", lambda: A.corm_attention(q, k, v, thr))):
-        ms = _events_time(fn, 5, 1)
-        res[name] = dict(ms=round(ms, 4), tflops=round(cfg.reference_flops() / (ms * 1e-3) / 1e12, 1))
+        ms, info = _variant(fn, 5)
+        res[name] = dict(ms=round(ms, 4), tflops=round(cfg.reference_flops() / (ms * 1e-3) / 1e12, 1), **info)
     # KeyFormer (kf.py): exp_rand [1, 32, 4096, 4096] fp32 (1 + |N(0,1)|, kf.py:48); its causal half is read twice
     # (row lse pass, column pass)
     er = 1 + torch.randn(cfg.B, cfg.Hq, cfg.Sq, cfg.Sk, device=dev).abs()
-    ms = _events_time(lambda: A.keyformer_attention(q, k, v, er), 5, 1)
+    ms, info = _variant(lambda: A.keyformer_attention(q, k, v, er), 5)
     er_bytes = 2 * cfg.B * cfg.Hq * (cfg.Sq * (cfg.Sq + 1) // 2) * 4
     res["cfg4_keyformer"] = dict(ms=round(ms, 4), tflops=round(cfg.reference_flops() / (ms * 1e-3) / 1e12, 1),
-                                 exp_rand_gbps=round(er_bytes / (ms * 1e-3) / 1e9, 1))
+                                 exp_rand_gbps=round(er_bytes / (ms * 1e-3) / 1e9, 1), **info)
     del er
     # RoCo's selection (models/roco.py:54-61) over the config-4 column sums with the e2e model's budget (512) and
     # recent window (256): the fused kernel against the reference's torch lines on the same GPU
@@ -265,16 +287,16 @@ def bench_variants(args, dev):
         pick = torch.topk(s1.gather(dim=-1, index=other) / S, dim=-1, k=512)[1]
         return torch.cat([other.gather(dim=-1, index=pick), recent], dim=-1).sort(dim=-1)[0]
 
-    ms = _events_time(lambda: A.roco_select(s1, s2, S, 256, 512), 20, 2)
-    ms_t = _events_time(roco_torch, 20, 2)
+    ms, info = _variant(lambda: A.roco_select(s1, s2, S, 256, 512), 20)
+    ms_t, _ = _variant(roco_torch, 20)
     nb = 2 * s1.numel() * 4 + s1.numel() // S * 768 * 8  # both sums read once, 768 indices written per row
     res["cfg4_roco_select"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1),
-                                   torch_us=round(ms_t * 1e3, 2))
+                                   torch_us=round(ms_t * 1e3, 2), **info)
     del s1, s2
     idx = A.topk_indices(A.h2o_attention(q, k, v)[1], cfg.topk)
-    ms = _events_time(lambda: A.kv_gather(k, v, idx), 20, 2)
+    ms, info = _variant(lambda: A.kv_gather(k, v, idx), 20)
     nb = 2 * 2 * idx.numel() * cfg.D * k.element_size()  # K and V rows read once and written once
-    res["cfg4_kv_gather_top256"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1))
+    res["cfg4_kv_gather_top256"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1), **info)
     return res
 
 

@@ -41,6 +41,7 @@ EXTRA_FLAGS = {
     # -amdgpu-mfma-vgpr-form: at one wave per SIMD (head_dim 256) LLVM otherwise writes MFMA results to AGPRs and
     # copies them out for the softmax; with it the head_dim-256 forward runs 0.98 instead of 1.09 ms (config 3)
     "attention.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp", "-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "attention_d256.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp", "-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

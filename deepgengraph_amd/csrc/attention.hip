@@ -1363,8 +1363,15 @@ void launch_fwd_d128(const AttnParams& p, hipStream_t st) {
 constexpr int kD256NW = 4, kD256BN = DGG_D256_BN, kD256NS = 2;
 constexpr int kD256BM = 32 * kD256NW;
 
+// DGG_D256_PIPE (default 1): the software-pipelined kernel of attention_d256.hip for the scores in fp32; 0 keeps
+// every head_dim-256 launch on attn_fwd_dma_kernel (for A/B measurements).
+#ifndef DGG_D256_PIPE
+#define DGG_D256_PIPE 1
+#endif
+
 template <typename T, bool MASK, bool SOFTCAP, int REFROUND>
 void launch_fwd_d256(const AttnParams& p, hipStream_t st) {
+  if (DGG_D256_PIPE && !REFROUND) return launch_attn_d256_pipe(p, std::is_same<T, BF16>::value, st);
   const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
   if (!REFROUND && p.lse == nullptr)
     hipLaunchKernelGGL((attn_fwd_dma_kernel<T, 256, 1, kD256NW, kD256BN, kD256NS, 1, MASK, SOFTCAP, REFROUND, !REFROUND>),

@@ -240,6 +240,15 @@ __device__ __forceinline__ float half_swap_sum(float x) {
 
 // Row-sum accumulation of 8 packed probabilities: l += sum of the rounded values, two per dot-product instruction.
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+// l + the two packed values (one dot-product instruction).
+__device__ __forceinline__ float dot2_ones(bf16x2 v, float l) {
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(v, one, l, false);
+}
+__device__ __forceinline__ float dot2_ones(f16x2 v, float l) {
+  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+  return __builtin_amdgcn_fdot2(v, one, l, false);
+}
 __device__ __forceinline__ float rowsum8(bf16x8 v, float l) {
   const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
   l = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 0, 1), one, l, false);
@@ -255,6 +264,10 @@ __device__ __forceinline__ float rowsum8(f16x8 v, float l) {
   return __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 6, 7), one, l, false);
 }
 
+
+// Software-pipelined head_dim-256 forward (attention_d256.hip) for 16-bit inputs without reference rounding:
+// 4 waves x 32 rows per workgroup (p.n_tiles counts 128-row query tiles).
+void launch_attn_d256_pipe(const AttnParams& p, bool bf16, hipStream_t st);
 
 // fp32 inputs (attention_f32.hip): the forward and the column-score pass, rows per workgroup tile of both.
 int f32_rows_per_tile();

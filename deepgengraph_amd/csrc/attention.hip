@@ -28,6 +28,12 @@
 
 #include "attention_common.h"
 
+// DGG_SPREAD_COPIES (default 1): mask-free tiles of the direct-load forward issue the next tile's copies among their
+// QK^T MFMAs; 0 issues them all right after the barrier (for A/B measurements).
+#ifndef DGG_SPREAD_COPIES
+#define DGG_SPREAD_COPIES 1
+#endif
+
 namespace {
 
 using namespace dgg_attn;
@@ -630,6 +636,20 @@ attn_fwd_dma_kernel(AttnParams p) {
     }
   };
 
+  // Load i (0 .. DMA_PER_TILE-1) of issue(t) for a tile whose rows all exist: the K loads, then the V loads. The
+  // mask-free tiles issue the next tile's copies one per QK^T step with these, so that the copies' issue overlaps
+  // the MFMAs instead of following the barrier as one burst (which held every wave of the workgroup at once).
+  auto issue_one = [&](int t, int i) __attribute__((always_inline)) {
+    const uint32_t kdst = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B + GPW * w * GROUP_B);
+    const int row0 = t * BN + 4 * GPW * w;
+    const int half = GPW * IPG, ii = i % half, j = ii / IPG, l = ii % IPG;
+    if (i < half)
+      dma16(kdst + j * GROUP_B + l * RPI * ROW_B, kp + (int64_t)row0 * k_ss_b + 4 * j * k_ss_b, k_voff[l]);
+    else
+      dma16(kdst + TILE_B + j * GROUP_B + l * RPI * ROW_B, vp + (int64_t)row0 * v_ss_b + 4 * j * v_ss_b, v_voff[l]);
+  };
+  static_assert(DMA_PER_TILE <= D / 16, "one copy per QK^T step");
+
   // LDS read addressing. K fragment (row mb*32 + r, chunk 2kk + g): lane part + xk[kk/2] + constant.
   // V transposing read (rows 16kk + 4g + (lane%16)/4 (+8), head-dim column db*32 + 16*((lane/16)%2) + 4*(lane%4)):
   // lane part + xv[db] + constant.
@@ -658,7 +678,9 @@ attn_fwd_dma_kernel(AttnParams p) {
   constexpr bool PK = REFROUND && !SOFTCAP && std::is_same<T, F16>::value;
   const float c = PK ? kLog2e : score_coeff<SOFTCAP, REFROUND>(p);
 
+  // SPREAD (mask-free tiles): the copies of tile t + NSTAGE - 1 are issued here, one per QK^T step.
   auto tile = [&](const int t, auto masked) {
+    constexpr bool SPREAD = !decltype(masked)::value && DGG_SPREAD_COPIES;
     const uint32_t st = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B);
     // Per-stage base addresses, opaque to the compiler so that every fragment read below is base + immediate
     // offset (otherwise it re-adds the stage offset for each read).
@@ -711,6 +733,9 @@ attn_fwd_dma_kernel(AttnParams p) {
     } else {
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) {
+        if constexpr (SPREAD) {
+          if (kk < DMA_PER_TILE) issue_one(t + NSTAGE - 1, kk);
+        }
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb) {
           const V8 a = lds_read<V8>(kbase[kk >> 1] + mb * 8 * GROUP_B + 32 * (kk & 1));
@@ -857,12 +882,20 @@ attn_fwd_dma_kernel(AttnParams p) {
     else if (NSTAGE >= 3 && after >= 1) wait_vmem<DMA_PER_TILE>();
     else wait_vmem<0>();
     __syncthreads();
-    if (t + NSTAGE - 1 < t_end) issue(t + NSTAGE - 1);
-    if (t >= wt_begin && t < wt_end) tile(t, masked);
+    constexpr bool SPREAD = !decltype(masked)::value && DGG_SPREAD_COPIES;
+    if (!SPREAD && t + NSTAGE - 1 < t_end) issue(t + NSTAGE - 1);
+    if (SPREAD || (t >= wt_begin && t < wt_end)) tile(t, masked);
   };
-  for (int t = t_begin; t < t_full0; ++t) step(t, std::true_type{});
-  for (int t = t_full0; t < t_full1; ++t) step(t, std::false_type{});
-  for (int t = t_full1; t < t_end; ++t) step(t, std::true_type{});
+  // Mask-free steps issue their copies inside the tile, so they are the tiles this wave computes whose copy target
+  // t + NSTAGE - 1 exists and is whole; the others (at most NSTAGE - 1 of them) take the masked step, which is
+  // correct for any tile.
+  int t_sp1 = t_full1;
+  if (DGG_SPREAD_COPIES) t_sp1 = min(min(t_full1, wt_end), min(t_end, p.Sk / BN) - (NSTAGE - 1));
+  const int t_sp0 = DGG_SPREAD_COPIES ? min(max(t_full0, wt_begin), t_end) : t_full0;
+  t_sp1 = max(t_sp0, t_sp1);
+  for (int t = t_begin; t < t_sp0; ++t) step(t, std::true_type{});
+  for (int t = t_sp0; t < t_sp1; ++t) step(t, std::false_type{});
+  for (int t = t_sp1; t < t_end; ++t) step(t, std::true_type{});
 
 #pragma unroll
   for (int n = 0; n < NQB; ++n) {

@@ -198,37 +198,69 @@ attn_fwd_d256_pipe_kernel(AttnParams p) {
     }
   };
 
-  // Soft-cap (exp2 domain), mask and row maximum of tile t in s, folded into m_run.
+  // Prepared form of a score. Without a soft-cap: the raw score x (its exp2-domain value is x * c). With one: the
+  // soft-cap's reciprocal r = 1 / (exp2(s * sc_a) + 1), of which the exp2-domain value x = sc_b - 2 sc_b r
+  // (softcap * tanh(s * scale / softcap) * log2(e)) is a decreasing function. The row maximum is then tracked as the
+  // minimum r, and the exponent x - m is one fma of r, so x itself is never formed. Masked scores: -inf / +inf.
+  const float sc_m2 = -2.0f * p.sc_b;
+  constexpr float MASKED_VAL = SOFTCAP ? INFINITY : -INFINITY;
+  // (With a soft-cap Q is pre-scaled by sc_a when it is loaded, so the MFMA yields s * sc_a directly; the scaled Q
+  // is rounded to the input dtype, a relative 2^-9 (bf16) of each score, as the reference's own rounding of the
+  // scores to the input dtype.)
+  auto prep_val = [&](float sraw) __attribute__((always_inline)) {
+    if constexpr (SOFTCAP) return fast_rcp(fast_exp2(sraw) + 1.0f);
+    else return sraw;
+  };
+  auto ext_upd = [&](float acc, float v) __attribute__((always_inline)) {
+    if constexpr (SOFTCAP) return fminf(acc, v);
+    else return fmaxf(acc, v);
+  };
+  auto ext_to_max = [&](float acc) __attribute__((always_inline)) {  // the row maximum (exp2 domain / c)
+    if constexpr (SOFTCAP) return fmaf(acc, sc_m2, p.sc_b);
+    else return acc;
+  };
+
+  // Soft-cap, mask and row maximum of tile t in s, folded into m_run.
   auto prep = [&](const int t, f32x16 (&s)[NMB], auto masked) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked)::value;
     const int kb4 = t * BN + 4 * g;
     const int rel_hi = k_hi - kb4, rel_lo = k_lo - kb4;
-    float mloc = -INFINITY;
+    float ext = MASKED_VAL;
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        float x = score_value<T, SOFTCAP, 0>(s[mb][j], p);
+        float x = prep_val(s[mb][j]);
         if constexpr (MASKED) {
           const int o = mb * 32 + 8 * (j >> 2) + (j & 3);
-          x = (o <= rel_hi && o >= rel_lo) ? x : -INFINITY;
+          x = (o <= rel_hi && o >= rel_lo) ? x : MASKED_VAL;
         }
         s[mb][j] = x;
-        mloc = fmaxf(mloc, x);
+        ext = ext_upd(ext, x);
       }
-    fold_max(mloc);
+    fold_max(ext_to_max(ext));
+  };
+  // exp2-domain exponent of a prepared score relative to the row's reference maximum: x * c - m * c; mcb is
+  // m * c (soft-cap: sc_b - m, c = 1).
+  auto rel_exp = [&](float v, float mcb) __attribute__((always_inline)) {
+    if constexpr (SOFTCAP) return fmaf(v, sc_m2, mcb);
+    else return fmaf(v, c, -mcb);
+  };
+  auto row_mcb = [&]() __attribute__((always_inline)) {
+    const float mc = m_run == -INFINITY ? 0.f : m_run * c;
+    return SOFTCAP ? p.sc_b - mc : mc;
   };
 
   // P = exp2(x*c - m*c) of a prepared tile, rounded to the storage type (pb[kk]: keys 16kk .. 16kk+15), and the
   // row sums.
   auto expo = [&](const f32x16 (&s)[NMB], V8 (&pb)[BN / 16]) __attribute__((always_inline)) {
-    const float mc = m_run == -INFINITY ? 0.f : m_run * c;
+    const float mcb = row_mcb();
 #pragma unroll
     for (int kk = 0; kk < BN / 16; ++kk) {
       f32x8 pv8;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float pe = fast_exp2(fmaf(s[kk >> 1][8 * (kk & 1) + e], c, -mc));
+        const float pe = fast_exp2(rel_exp(s[kk >> 1][8 * (kk & 1) + e], mcb));
         if constexpr (!FASTSUM) l_part[e & 1] += pe;
         pv8[e] = pe;
       }
@@ -287,7 +319,7 @@ attn_fwd_d256_pipe_kernel(AttnParams p) {
       const int kk = i >> 3, db = i & 7;
       return vbs[db & 3] + 256 * (db >> 2) + kk * 4 * GROUP_B;
     };
-    const float mc = m_run == -INFINITY ? 0.f : m_run * c;
+    const float mcb = row_mcb();
     V8 ka[PF + 1];
 #pragma unroll
     for (int i = 0; i < PF; ++i) ka[i] = lds_read<V8>(kaddr(i));
@@ -307,7 +339,7 @@ attn_fwd_d256_pipe_kernel(AttnParams p) {
       if (i + PF < 32) ka[(i + PF) % (PF + 1)] = lds_read<V8>(kaddr(i + PF));
       sn[i & 1] = mfma32(ka[i % (PF + 1)], qf[i >> 1], sn[i & 1]);
       const int kk = i >> 3, e = i & 7;
-      const float pe = fast_exp2(fmaf(sc[kk >> 1][8 * (kk & 1) + e], c, -mc));
+      const float pe = fast_exp2(rel_exp(sc[kk >> 1][8 * (kk & 1) + e], mcb));
       if constexpr (!FASTSUM) l_part[e & 1] += pe;
       if (e & 1) {
         pw[kk][e >> 1] = __builtin_convertvector(f32x2{pe_even, pe}, H2);
@@ -328,7 +360,7 @@ attn_fwd_d256_pipe_kernel(AttnParams p) {
       va[i][0] = tr_read_at(vaddr(i), S{});
       va[i][1] = tr_read_at(vaddr(i) + 2 * GROUP_B, S{});
     }
-    float mloc = -INFINITY;
+    float ext = MASKED_VAL;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
       if (i + PF < 32) {
@@ -337,12 +369,12 @@ attn_fwd_d256_pipe_kernel(AttnParams p) {
       }
       const V8 a = __builtin_shufflevector(va[i % (PF + 1)][0], va[i % (PF + 1)][1], 0, 1, 2, 3, 4, 5, 6, 7);
       oacc[i & 7] = mfma32(a, pb[i >> 3], oacc[i & 7]);
-      const float x = score_value<T, SOFTCAP, 0>(sn[i >> 4][i & 15], p);
+      const float x = prep_val(sn[i >> 4][i & 15]);
       sn[i >> 4][i & 15] = x;
-      mloc = fmaxf(mloc, x);
+      ext = ext_upd(ext, x);
       __builtin_amdgcn_sched_barrier(0);
     }
-    fold_max(mloc);
+    fold_max(ext_to_max(ext));
   };
 
   // Pipeline iteration t (on entry tile t is prepared in scur: soft-capped, masked, its maximum folded into m_run):
@@ -395,6 +427,7 @@ attn_fwd_d256_pipe_kernel(AttnParams p) {
     for (int kk = 0; kk < D / 16; ++kk) {
       asm volatile("" : "+v"(qf[kk]));
       if (!live) qf[kk] = V8{};
+      if constexpr (SOFTCAP) qf[kk] = from_f32x8<V8>(to_f32x8(qf[kk]) * p.sc_a);
       asm volatile("" : "+a"(qf[kk]));
     }
     if (t_begin + 1 < t_end) wait_vmem<2 * DMA_PER_TILE>();  // K(t_begin) has landed

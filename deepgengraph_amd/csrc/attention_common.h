@@ -179,6 +179,25 @@ __device__ __forceinline__ void map_block(int n_tiles, int bh_count, bool revers
   bh = bh_minor;
 }
 
+// Forward kernels with grouped query heads (Hq = G * Hkv, G > 1) and B * Hkv divisible by 8: each XCD takes whole
+// KV heads, one after the other, and within a KV head the query tiles longest first with the G query heads of a
+// tile next to each other. The workgroups resident on an XCD at a time are then adjacent query tiles of the query
+// heads of one KV head, whose K/V windows overlap: fewer K/V bytes pass through that XCD's L2 per generation of
+// workgroups than with the heads of two KV heads side by side (map_block). Otherwise map_block's order.
+__device__ __forceinline__ void map_block_kv(int n_tiles, int B, int Hq, int Hkv, bool reverse, int& tile, int& bh) {
+  const int G = Hq / Hkv, nkv = B * Hkv;
+  if (G == 1 || (nkv & 7) != 0) return map_block(n_tiles, B * Hq, reverse, tile, bh);
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7, local = bid >> 3;
+  const int per_kv = n_tiles * G;
+  const int kv_local = local / per_kv, rem = local - kv_local * per_kv;
+  const int t_major = rem / G, qh = rem - t_major * G;
+  const int kvi = xcd * (nkv >> 3) + kv_local;  // b * Hkv + hk
+  const int b = kvi / Hkv, hk = kvi - b * Hkv;
+  bh = b * Hq + hk * G + qh;
+  tile = reverse ? n_tiles - 1 - t_major : t_major;
+}
+
 // ------------------------------------------------------------------------------------------------
 // Forward kernel for head_dim 128 and 256 ("DMA kernel"). NW waves of 32*NQB query rows each; K/V tiles of BN
 // keys are copied global -> LDS by the direct-to-LDS loads of gfx950 (no VGPR staging, no LDS store

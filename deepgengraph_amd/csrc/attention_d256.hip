@@ -45,7 +45,7 @@ attn_fwd_d256_pipe_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[4 * TILE_B];  // K slot 0, K slot 1, V slot 0, V slot 1
 
   int qt, bh;
-  map_block(p.n_tiles, p.B * p.Hq, true, qt, bh);
+  map_block_kv(p.n_tiles, p.B, p.Hq, p.Hkv, true, qt, bh);
   const int b = bh / p.Hq, h = bh - b * p.Hq;
   const int hk = h / p.group;
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 31, g = lane >> 5;

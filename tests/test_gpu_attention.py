@@ -66,6 +66,29 @@ def test_prefill_matches_oracle(gpu, B, Sq, Sk, Hq, Hkv, D, dtype, causal, softc
     assert_close(lse_c[fin], ref_lse[fin], 2e-2, 1e-2, what + " lse")
 
 
+# Grouped-query head_dim-256 launches at sizes where an XCD runs more than one generation of workgroups per KV
+# head (the KV-head order of map_block_kv: more than 32 workgroups per KV head), checked on a few whole heads.
+GQA_LARGE_CASES = [
+    # B, Sq, Sk, Hq, Hkv, dtype, causal, softcap, window
+    (1, 2500, 2500, 16, 8, torch.bfloat16, True, 50.0, 1000),   # soft-cap + window, ragged Sk
+    (1, 2300, 2333, 16, 8, torch.float16, False, 0.0, 0),       # non-causal, Sq != Sk
+    (1, 2200, 2600, 16, 8, torch.bfloat16, True, 0.0, 0),       # bottom-right causal
+]
+
+
+@pytest.mark.parametrize("B,Sq,Sk,Hq,Hkv,dtype,causal,softcap,window", GQA_LARGE_CASES)
+def test_prefill_d256_gqa_large_kv_order(gpu, B, Sq, Sk, Hq, Hkv, dtype, causal, softcap, window):
+    D = 256
+    q, k, v = _qkv(B, Sq, Sk, Hq, Hkv, D, dtype, seed=Sq + 3 * Sk)
+    out = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), causal=causal, softcap=softcap, window=window).cpu()
+    G = Hq // Hkv
+    for h in (0, 5, Hq - 1):
+        ref = oa.attention(q[:, :, h:h + 1], k[:, :, h // G:h // G + 1], v[:, :, h // G:h // G + 1], causal=causal,
+                           softcap=softcap or None, window=window or None)
+        what = f"Sq{Sq} Sk{Sk} H{Hq}/{Hkv} {dtype} causal={causal} cap={softcap} win={window} head {h}"
+        assert_close(out[:, :, h:h + 1].float(), ref.float(), *TOL[dtype], what)
+
+
 FAST_CASES = [
     # bf16, head_dim 128, no lse / soft-cap / reference rounding: B, Sq, Sk, Hq, Hkv, causal, window
     (1, 512, 512, 2, 2, True, 0),

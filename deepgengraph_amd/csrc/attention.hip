@@ -1209,8 +1209,74 @@ attn_colsum_d128_kernel(AttnParams p) {
   // Corm's thresholds of (row, kjc), addressed the same way.
   const uint32_t thr_lane_b = EPI == kColAnyGe ? (uint32_t)((4 * g * p.thr_rs + kjc) * 4) : 0u;
 
-  auto tile = [&](const int t, auto masked) {
+  // S = Q . K^T of query tile t (its LDS stage) into s.
+  auto qk_t = [&](const int t, f32x16 (&s)[NMB]) __attribute__((always_inline)) {
     const uint32_t st = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B);
+    uint32_t qb[4];  // opaque per-stage bases (reads at base + immediate offset)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      qb[i] = st + xq[i];
+      if constexpr (NSTAGE == 3) asm volatile("" : "+v"(qb[i]));
+    }
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) s[mb] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb) {
+        const V8 a = lds_read<V8>(qb[kk >> 1] + mb * 8 * GROUP_B + 32 * (kk & 1));
+        s[mb] = mfma32(a, kf[kk], s[mb]);
+      }
+    }
+  };
+  auto epi_t = [&](const int t, const f32x16 (&sacc)[NMB], const float (&ev)[NMB][16], const float (&tv)[NMB][16],
+                   auto masked) __attribute__((always_inline)) {
+    uint32_t lb = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B) + QT_B + 16 * g;  // this lane's lse values
+    if constexpr (NSTAGE == 3) asm volatile("" : "+v"(lb));
+    // Visibility of (row o of the tile, this lane's key): causal rel >= 0, window rel < window, row < Sq.
+    const int rel0 = t * BQ + 4 * g + p.offset - kj;
+    const int rows_left = p.Sq - t * BQ - 4 * g;
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) {
+      f32x4 lv[4];
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) lv[jq] = lds_read<f32x4>(lb + 4 * (32 * mb + 8 * jq));
+      f16x2 hs[8];
+      if constexpr (PK) {
+#pragma unroll
+        for (int jp = 0; jp < 8; ++jp) hs[jp] = ref_scores_f16(sacc[mb][2 * jp], sacc[mb][2 * jp + 1], p);
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float x;
+        if constexpr (PK) x = (float)hs[j >> 1][j & 1];
+        else x = score_value<T, SOFTCAP, REFROUND>(sacc[mb][j], p);
+        const float l2 = LSE2 ? lv[j >> 2][j & 3] : lv[j >> 2][j & 3] * kLog2e;
+        const int o = 32 * mb + 8 * (j >> 2) + (j & 3);
+        float pe;
+        if constexpr (EPI == kColKF)
+          pe = kf_prob(x * c, ev[mb][j], l2, p);
+        else
+          pe = fast_exp2(fmaf(x, c, -l2));
+        bool valid = true, vis = true;
+        if constexpr (decltype(masked)::value) {
+          valid = o < rows_left;
+          bool ok = valid;
+          if constexpr (MASK) {
+            if (p.causal) ok = ok && rel0 + o >= 0;
+            if (p.window > 0) ok = ok && rel0 + o < p.window;
+          }
+          pe = ok ? pe : 0.f;
+          vis = ok;
+        }
+        // Corm compares visible pairs here; the masked ones (p = 0) are ORed in by corm_masked_or_kernel
+        if constexpr (EPI == kColAnyGe) acc.any |= vis && pe >= tv[mb][j];
+        else acc.add(pe, valid, min(t * BQ + 4 * g + o, p.Sq - 1), kjc, p);
+      }
+    }
+  };
+
+  auto tile = [&](const int t, auto masked) {
     float ev[NMB][16];
     if constexpr (EPI == kColKF) {
       if constexpr (!decltype(masked)::value) {  // every row of the tile exists (and er_lane32 holds)
@@ -1256,57 +1322,8 @@ attn_colsum_d128_kernel(AttnParams p) {
       }
     }
     f32x16 sacc[NMB];
-#pragma unroll
-    for (int mb = 0; mb < NMB; ++mb) sacc[mb] = f32x16{};
-#pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) {
-#pragma unroll
-      for (int mb = 0; mb < NMB; ++mb) {
-        const V8 a = lds_read<V8>(st + xq[kk >> 1] + mb * 8 * GROUP_B + 32 * (kk & 1));
-        sacc[mb] = mfma32(a, kf[kk], sacc[mb]);
-      }
-    }
-    // Visibility of (row o of the tile, this lane's key): causal rel >= 0, window rel < window, row < Sq.
-    const int rel0 = t * BQ + 4 * g + p.offset - kj;
-    const int rows_left = p.Sq - t * BQ - 4 * g;
-#pragma unroll
-    for (int mb = 0; mb < NMB; ++mb) {
-      f32x4 lv[4];
-#pragma unroll
-      for (int jq = 0; jq < 4; ++jq) lv[jq] = lds_read<f32x4>(st + QT_B + 4 * (32 * mb + 8 * jq + 4 * g));
-      f16x2 hs[8];
-      if constexpr (PK) {
-#pragma unroll
-        for (int jp = 0; jp < 8; ++jp) hs[jp] = ref_scores_f16(sacc[mb][2 * jp], sacc[mb][2 * jp + 1], p);
-      }
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        float x;
-        if constexpr (PK) x = (float)hs[j >> 1][j & 1];
-        else x = score_value<T, SOFTCAP, REFROUND>(sacc[mb][j], p);
-        const float l2 = LSE2 ? lv[j >> 2][j & 3] : lv[j >> 2][j & 3] * kLog2e;
-        const int o = 32 * mb + 8 * (j >> 2) + (j & 3);
-        float pe;
-        if constexpr (EPI == kColKF)
-          pe = kf_prob(x * c, ev[mb][j], l2, p);
-        else
-          pe = fast_exp2(fmaf(x, c, -l2));
-        bool valid = true, vis = true;
-        if constexpr (decltype(masked)::value) {
-          valid = o < rows_left;
-          bool ok = valid;
-          if constexpr (MASK) {
-            if (p.causal) ok = ok && rel0 + o >= 0;
-            if (p.window > 0) ok = ok && rel0 + o < p.window;
-          }
-          pe = ok ? pe : 0.f;
-          vis = ok;
-        }
-        // Corm compares visible pairs here; the masked ones (p = 0) are ORed in by corm_masked_or_kernel
-        if constexpr (EPI == kColAnyGe) acc.any |= vis && pe >= tv[mb][j];
-        else acc.add(pe, valid, min(t * BQ + 4 * g + o, p.Sq - 1), kjc, p);
-      }
-    }
+    qk_t(t, sacc);
+    epi_t(t, sacc, ev, tv, masked);
   };
 
 #pragma unroll
@@ -1314,9 +1331,74 @@ attn_colsum_d128_kernel(AttnParams p) {
     if (t_begin + i < t_end) issue(t_begin + i);
   // Corm: whether this wave's keys are all decided (no tile of its range left, or every key flagged).
   bool wave_done = wt_begin >= wt_end;
-  auto step = [&](const int t, auto masked) -> bool {
+  // One pipelined step: the mask-free epilogue of tile t (scores in sc) and S of tile t+1 (into sn), in a fixed
+  // order of 32 fenced steps, one per MFMA: the Q fragment read two steps ahead, the QK^T MFMA (k-step i/4, block
+  // i%4), the exponentials and sums of score pair i%8 of block i/8, and every second step the lse values of the
+  // pairs two steps ahead. (Left to the compiler, the 32 fragment reads move to the front and the form spills.)
+  auto pipe_step = [&](const int t, const f32x16 (&sc)[NMB], f32x16 (&sn)[NMB]) __attribute__((always_inline)) {
+    static_assert(NMB == 4, "32 steps: 8 k-steps x 4 blocks, 4 blocks x 8 score pairs");
+    const uint32_t stc = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B);
+    const uint32_t stn = smem_base + (uint32_t)(((t + 1) % NSTAGE) * STAGE_B);
+    // per-stage base registers, opaque to the compiler, so that every read is base + immediate offset
+    uint32_t qb[4], lb = stc + QT_B + 16 * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      qb[i] = stn + xq[i];
+      asm volatile("" : "+v"(qb[i]));
+    }
+    asm volatile("" : "+v"(lb));
+    auto qread = [&](const int i) __attribute__((always_inline)) {
+      const int kk = i >> 2, mb = i & 3;
+      return lds_read<V8>(qb[kk >> 1] + mb * 8 * GROUP_B + 32 * (kk & 1));
+    };
+    auto lread = [&](const int i) __attribute__((always_inline)) {  // lse of the rows of pairs i, i+1 (i even)
+      return lds_read<f32x4>(lb + 4 * (32 * (i >> 3) + 8 * ((i & 7) >> 1)));
+    };
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) sn[mb] = f32x16{};
+    V8 a[3];
+    f32x4 lvb[2];
+    a[0] = qread(0);
+    a[1] = qread(1);
+    lvb[0] = lread(0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      if (i + 2 < 32) a[(i + 2) % 3] = qread(i + 2);
+      if ((i & 1) == 0 && i + 2 < 32) lvb[((i + 2) >> 1) & 1] = lread(i + 2);
+      sn[i & 3] = mfma32(a[i % 3], kf[i >> 2], sn[i & 3]);
+      const int mb = i >> 3, jp = i & 7;
+      const f32x4& lv = lvb[(i >> 1) & 1];
+      float x[2];
+      if constexpr (PK) {
+        const f16x2 hs = ref_scores_f16(sc[mb][2 * jp], sc[mb][2 * jp + 1], p);
+        x[0] = (float)hs[0];
+        x[1] = (float)hs[1];
+      } else {
+        x[0] = score_value<T, SOFTCAP, REFROUND>(sc[mb][2 * jp], p);
+        x[1] = score_value<T, SOFTCAP, REFROUND>(sc[mb][2 * jp + 1], p);
+      }
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float l2 = LSE2 ? lv[2 * (jp & 1) + e] : lv[2 * (jp & 1) + e] * kLog2e;
+        acc.add(fast_exp2(fmaf(x[e], c, -l2)), true, 0, kjc, p);
+      }
+      acc.pin();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // PIPE: the mask-free tiles of a wave run software-pipelined, the QK^T MFMAs of tile t+1 in the same basic block
+  // as the exponentials and sums of tile t (which are VALU work the MFMA pipe would otherwise wait out). Tile t+1
+  // must then be in the LDS at the barrier of tile t, so every barrier waits for all copies issued before it, and
+  // a third stage keeps tile t (its lse values) while tile t+2 lands.
+  constexpr bool PIPE = NSTAGE == 3;
+  static_assert(!PIPE || EPI == kColSum || EPI == kColSumSq, "three stages only for the pipelined epilogues");
+  // Waits for the copies of tile t (PIPE: and of tile t+1), then the barrier after which tile t+NSTAGE-1 is
+  // requested into the stage of tile t-1 (every wave has finished with it).
+  auto sync = [&](const int t) -> bool {
     // Tiles t+1 .. t+after may stay in flight; the last wave issues NLSE more copies per tile.
-    const int after = min(NSTAGE - 2, t_end - 1 - t);
+    const int after = PIPE ? 0 : min(NSTAGE - 2, t_end - 1 - t);
     if (w == NW - 1) {
       if (NSTAGE >= 4 && after >= 2) wait_vmem<2 * (GPW + NLSE)>();
       else if (NSTAGE >= 3 && after >= 1) wait_vmem<GPW + NLSE>();
@@ -1336,6 +1418,10 @@ attn_colsum_d128_kernel(AttnParams p) {
       __syncthreads();
     }
     if (t + NSTAGE - 1 < t_end) issue(t + NSTAGE - 1);
+    return true;
+  };
+  auto step = [&](const int t, auto masked) -> bool {
+    if (!sync(t)) return false;
     if (t >= wt_begin && t < wt_end) {
       tile(t, masked);
       if constexpr (EPI == kColAnyGe) {
@@ -1348,7 +1434,33 @@ attn_colsum_d128_kernel(AttnParams p) {
   };
   bool go = true;
   for (int t = t_begin; go && t < t_full0; ++t) go = step(t, std::true_type{});
-  for (int t = t_full0; go && t < t_full1; ++t) go = step(t, std::false_type{});
+  // The mask-free range lies inside the wave's range whenever the wave has keys (kw0 < Sk).
+  if (PIPE && t_full1 - t_full0 >= 2 && t_full0 >= wt_begin && t_full1 <= wt_end) {
+    // scores of two tiles in flight, in two buffers that swap roles every step (loop unrolled by two)
+    f32x16 sa[NMB], sb[NMB];
+    float none[NMB][16];  // KeyFormer / Corm inputs, never read by these epilogues
+    int t = t_full0;
+    sync(t);
+    qk_t(t, sa);
+    pipe_step(t, sa, sb);
+    for (++t;;) {
+      sync(t);
+      if (t + 1 >= t_full1) {
+        epi_t(t, sb, none, none, std::false_type{});
+        break;
+      }
+      pipe_step(t, sb, sa);
+      sync(++t);
+      if (t + 1 >= t_full1) {
+        epi_t(t, sa, none, none, std::false_type{});
+        break;
+      }
+      pipe_step(t, sa, sb);
+      ++t;
+    }
+  } else {
+    for (int t = t_full0; go && t < t_full1; ++t) go = step(t, std::false_type{});
+  }
   for (int t = t_full1; go && t < t_end; ++t) go = step(t, std::true_type{});
 
   acc.store(p, bh, kj, g);
@@ -1445,17 +1557,23 @@ void pick_fwd(const AttnParams& p, bool ref, hipStream_t st) {
   }
 }
 // head_dim 128 column sums (measured on MI355X, config 4): 8 waves x 32 keys, 128-row query tiles, 2 stages.
+// DGG_COL_PIPE (default 1): the sum epilogues (H2O / SnapKV, RoCo) run the software-pipelined 3-stage form.
+#ifndef DGG_COL_PIPE
+#define DGG_COL_PIPE 1
+#endif
 constexpr int kC128NW = 8, kC128BQ = 128, kC128NS = 2;
 constexpr int kC128BK = 32 * kC128NW;  // keys per workgroup (head_dim 128)
 
 template <typename T, bool MASK, bool SOFTCAP, int REFROUND, int EPI>
 void launch_colsum_d128(const AttnParams& p, hipStream_t st) {
   const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
+  // (the reference-rounded soft-cap's score chain is too long for a fixed-order step: it keeps the plain form)
+  constexpr int NS = DGG_COL_PIPE && (EPI == kColSum || EPI == kColSumSq) && !(SOFTCAP && REFROUND) ? 3 : kC128NS;
   if (p.lse_base2)
-    hipLaunchKernelGGL((attn_colsum_d128_kernel<T, kC128NW, kC128BQ, kC128NS, MASK, SOFTCAP, REFROUND, true, EPI>),
+    hipLaunchKernelGGL((attn_colsum_d128_kernel<T, kC128NW, kC128BQ, NS, MASK, SOFTCAP, REFROUND, true, EPI>),
                        dim3(grid), dim3(64 * kC128NW), 0, st, p);
   else
-    hipLaunchKernelGGL((attn_colsum_d128_kernel<T, kC128NW, kC128BQ, kC128NS, MASK, SOFTCAP, REFROUND, false, EPI>),
+    hipLaunchKernelGGL((attn_colsum_d128_kernel<T, kC128NW, kC128BQ, NS, MASK, SOFTCAP, REFROUND, false, EPI>),
                        dim3(grid), dim3(64 * kC128NW), 0, st, p);
 }
 

@@ -134,6 +134,12 @@ struct ColAcc {
       if constexpr (EPI == kColSumSq) s2 = fmaf(pe, pe, s2);
     }
   }
+  // Ties the sums so far to this point of the program (a fixed-order schedule would otherwise see its additions
+  // sunk past later code that does not use them).
+  __device__ __forceinline__ void pin() {
+    if constexpr (EPI != kColAnyGe) asm volatile("" : "+v"(s));
+    if constexpr (EPI == kColSumSq) asm volatile("" : "+v"(s2));
+  }
   // Combines the two lane halves (rows 4g..) and stores column kj of (batch, head) bh.
   __device__ __forceinline__ void store(const AttnParams& p, int bh, int kj, int g) {
     if constexpr (EPI == kColAnyGe) {

@@ -339,6 +339,10 @@ def _colsum_reference(q, k, causal, softcap, window):
     (128, 517, 333, True, 0, 0.0, torch.bfloat16, False),   # Sq > Sk: leading rows see no key
     (128, 300, 300, False, 0, 0.0, torch.float16, True),
     (128, 640, 640, True, 100, 0.0, torch.float16, True),
+    # long runs of mask-free query tiles (the software-pipelined column pass), ragged ends, Sq < Sk
+    (128, 1100, 1300, True, 700, 0.0, torch.float16, True),
+    (128, 1024, 1024, False, 0, 0.0, torch.bfloat16, False),
+    (128, 900, 900, True, 0, 30.0, torch.bfloat16, True),
     (256, 160, 160, True, 0, 30.0, torch.bfloat16, False),
     (256, 300, 300, True, 64, 50.0, torch.float16, True),
 ])

@@ -164,3 +164,55 @@ def test_kernel_reference_rounding_on_crafted_scores(gpu, dtype):
     got, want = lse.cpu()[0, 0].double(), ref_lse[0, 0].double()
     err = ((got - want).abs() / want.abs().clamp_min(1e-3)).max().item()
     assert err < 2e-6, f"max relative lse error {err:.3e} (one 16-bit ulp of a score is ~1e-3)"
+
+
+def _kernel_multiplier(d: float) -> np.float32:
+    """The fp32 multiplier the library uses for scale = 1 / d: the divisor is recovered from the fp32 scale as
+    RN32(1 / scale) (sqrt(D) itself for the default scale) and its fp32 reciprocal taken."""
+    sf = np.float32(1.0 / d)
+    div = np.float32(d) if d == math.sqrt(128) else np.float32(1.0 / np.float64(sf))
+    return np.float32(1.0) / div
+
+
+def _double_rounding_divisor() -> float:
+    """A divisor whose fp16 multiply RN16(RN32(x * r)) differs from the single rounding RN16(x * r) for some x
+    (about one multiplier in a hundred does; none of the 1/sqrt(D) defaults): where a kernel that rounded the
+    exact product once (as the fp16 mixed-multiply instructions do) would be wrong."""
+    x = _all_values(torch.float16)
+    for i in range(2000):
+        d = 3.0 + 0.00731 * i
+        r = _kernel_multiplier(d)
+        twice = _round16(x * r, torch.float16)
+        once = (x.astype(np.float64) * np.float64(r)).astype(np.float16).astype(np.float32)
+        if not _same_bits(twice, once):
+            return d
+    raise AssertionError("no such divisor found")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("which", ["default", "double_rounding"])
+def test_kernel_fp16_multiply_on_every_value(gpu, which):
+    """Every finite fp16 value x as the one score of a row (q = [x, 0, ...], one key [1, 0, ...]): the fp16
+    reference-rounding forward at head_dim 128 must give lse = RN16(RN32(x * r)), for the default divisor and for
+    a divisor whose multiplier rounds differently when the exact product is rounded once."""
+    from deepgengraph_amd import attention as A
+
+    d = math.sqrt(128) if which == "default" else _double_rounding_divisor()
+    r = _kernel_multiplier(d)
+    x = _all_values(torch.float16)
+    want = _round16(x * r, torch.float16).astype(np.float64)
+    once = (x.astype(np.float64) * np.float64(r)).astype(np.float16).astype(np.float64)
+    D = 128
+    q = np.zeros((1, x.size, 1, D), np.float32)
+    q[0, :, 0, 0] = x
+    k = np.zeros((1, 1, 1, D), np.float32)
+    k[0, 0, 0, 0] = 1.0
+    qg = torch.from_numpy(q).to(torch.float16).to(gpu)
+    kg = torch.from_numpy(k).to(torch.float16).to(gpu)
+    _, lse = A.attention(qg, kg, kg, causal=False, return_lse=True, ref_rounding=True,
+                         scale=None if which == "default" else 1.0 / d)
+    got = lse.cpu()[0, 0].double().numpy()
+    rel = np.abs(got - want) / np.maximum(np.abs(want), 1e-3)
+    assert rel.max() < 2e-6, f"{which}: max relative lse error {rel.max():.3e} at x = {x[rel.argmax()]}"
+    if which == "double_rounding":  # the check can tell the two roundings apart
+        assert (np.abs(once - want) / np.maximum(np.abs(want), 1e-3)).max() > 1e-4

@@ -204,6 +204,28 @@ __device__ __forceinline__ void map_block_kv(int n_tiles, int B, int Hq, int Hkv
   tile = reverse ? n_tiles - 1 - t_major : t_major;
 }
 
+// map_block_kv's grouping with a causal sliding window. The first KV head an XCD takes runs its query tiles in
+// ascending order: its shorter tiles below the window first (all starting at key 0), then the whole-window tiles,
+// each generation of workgroups starting on keys the previous one touched last, which the XCD's L2 still holds.
+// A second KV head runs its whole-window tiles (full0 ..) in ascending order and then its shorter tiles longest
+// first, so that the XCD's last workgroups are short and the launch ends evenly.
+__device__ __forceinline__ void map_block_kv_window(int n_tiles, int B, int Hq, int Hkv, int full0, int& tile,
+                                                    int& bh) {
+  const int G = Hq / Hkv, nkv = B * Hkv;
+  if (G == 1 || (nkv & 7) != 0) return map_block(n_tiles, B * Hq, true, tile, bh);
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7, local = bid >> 3;
+  const int per_kv = n_tiles * G;
+  const int kv_local = local / per_kv, rem = local - kv_local * per_kv;
+  const int t_major = rem / G, qh = rem - t_major * G;
+  const int kvi = xcd * (nkv >> 3) + kv_local;  // b * Hkv + hk
+  const int b = kvi / Hkv, hk = kvi - b * Hkv;
+  bh = b * Hq + hk * G + qh;
+  const int nfull = n_tiles - full0;
+  if ((kv_local & 1) == 0) tile = t_major;
+  else tile = t_major < nfull ? full0 + t_major : full0 - 1 - (t_major - nfull);
+}
+
 // ------------------------------------------------------------------------------------------------
 // Forward kernel for head_dim 128 and 256 ("DMA kernel"). NW waves of 32*NQB query rows each; K/V tiles of BN
 // keys are copied global -> LDS by the direct-to-LDS loads of gfx950 (no VGPR staging, no LDS store

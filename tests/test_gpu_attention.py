@@ -67,12 +67,18 @@ def test_prefill_matches_oracle(gpu, B, Sq, Sk, Hq, Hkv, D, dtype, causal, softc
 
 
 # Grouped-query head_dim-256 launches at sizes where an XCD runs more than one generation of workgroups per KV
-# head (the KV-head order of map_block_kv: more than 32 workgroups per KV head), checked on a few whole heads.
+# head (the KV-head orders of map_block_kv / map_block_kv_window: more than 32 workgroups per KV head), checked on
+# a few whole heads.
 GQA_LARGE_CASES = [
     # B, Sq, Sk, Hq, Hkv, dtype, causal, softcap, window
     (1, 2500, 2500, 16, 8, torch.bfloat16, True, 50.0, 1000),   # soft-cap + window, ragged Sk
     (1, 2300, 2333, 16, 8, torch.float16, False, 0.0, 0),       # non-causal, Sq != Sk
     (1, 2200, 2600, 16, 8, torch.bfloat16, True, 0.0, 0),       # bottom-right causal
+    # B * Hkv = 16: two KV heads per XCD, a causal window, so both query-tile orders of map_block_kv_window run
+    # (ascending for the first KV head of an XCD, whole-window tiles then the shorter ones for the second; head 15
+    # reads KV head 7, a second one)
+    (2, 1500, 1500, 16, 8, torch.bfloat16, True, 30.0, 600),
+    (2, 1400, 1700, 16, 8, torch.float16, True, 0.0, 900),      # Sq < Sk: the window start moves with the offset
 ]
 
 

@@ -357,7 +357,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
     }
   };
 
-  const float c = score_coeff<false, REFROUND>(p);
+  // fp16 reference rounding keeps each pair of scores packed (two instructions per score instead of four)
+  constexpr bool PK = REFROUND && std::is_same<T, F16>::value;
+  const float cy = (PK ? kLog2e : score_coeff<false, REFROUND>(p)) * p.kf_inv_tau;  // score -> exp2 domain / tau
+  f16x2 hpair;
   float m_run = -INFINITY, l_run = 0.f;
   // element (mb, j) of the S^T accumulators holds key t*BN + mb*32 + 8*(j/4) + 4g + j%4. The exp_rand values of
   // tile t+1 are loaded while tile t is computed (ev_next), so the stream stays in flight under the exp/log work.
@@ -394,8 +397,16 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
     for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const float x2 = score_value<T, false, REFROUND>(sacc[mb][j], p) * c;
-        float y = (x2 - fast_log2(ev[mb][j >> 2][j & 3])) * p.kf_inv_tau;
+        // y = (x2 - log2 e) / tau as one fma of the score against per-launch constants: the score x in the natural
+        // log domain times log2(e) / tau (PK: the reference-rounded fp16 pair, read by v_fma_mix), or x * c / tau
+        float x;
+        if constexpr (PK) {
+          if ((j & 1) == 0) hpair = ref_scores_f16(sacc[mb][j], sacc[mb][j + 1], p);
+          x = (float)hpair[j & 1];
+        } else {
+          x = score_value<T, false, REFROUND>(sacc[mb][j], p);
+        }
+        float y = fmaf(x, cy, -fast_log2(ev[mb][j >> 2][j & 3]) * p.kf_inv_tau);
         if constexpr (decltype(masked)::value) {
           const int o = mb * 32 + 8 * (j >> 2) + (j & 3);
           y = (o <= rel_hi && o >= rel_lo) ? y : -INFINITY;
@@ -1200,6 +1211,7 @@ attn_colsum_d128_kernel(AttnParams p) {
 
   constexpr bool PK = REFROUND && !SOFTCAP && std::is_same<T, F16>::value;
   const float c = PK ? kLog2e : score_coeff<SOFTCAP, REFROUND>(p);
+  const float cy = EPI == kColKF ? c * p.kf_inv_tau : 0.f;  // KeyFormer: score -> exp2 domain / tau
   ColAcc<EPI> acc;
   const int kjc = min(kj, p.Sk - 1);
   const float* erp = EPI == kColKF ? p.er + b * p.er_sb + h * p.er_sh : nullptr;  // KeyFormer exp_rand of (b, h)
@@ -1254,8 +1266,8 @@ attn_colsum_d128_kernel(AttnParams p) {
         const float l2 = LSE2 ? lv[j >> 2][j & 3] : lv[j >> 2][j & 3] * kLog2e;
         const int o = 32 * mb + 8 * (j >> 2) + (j & 3);
         float pe;
-        if constexpr (EPI == kColKF)
-          pe = kf_prob(x * c, ev[mb][j], l2, p);
+        if constexpr (EPI == kColKF)  // kf_prob with x * c folded into one fma against c / tau
+          pe = __builtin_amdgcn_exp2f(fmaf(x, cy, -fmaf(__builtin_amdgcn_logf(ev[mb][j]), p.kf_inv_tau, l2)));
         else
           pe = fast_exp2(fmaf(x, c, -l2));
         bool valid = true, vis = true;

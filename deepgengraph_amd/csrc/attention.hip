@@ -365,24 +365,48 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   // element (mb, j) of the S^T accumulators holds key t*BN + mb*32 + 8*(j/4) + 4g + j%4. The exp_rand values of
   // tile t+1 are loaded while tile t is computed (ev_next), so the stream stays in flight under the exp/log work.
   f32x4 ev[NMB][4], ev_next[NMB][4];
+  // Tiles whose keys all exist (VEC: rows 16-byte aligned) load exp_rand coalesced: load i of lane l reads keys
+  // 4 (l % 16) .. +3 of the wave's row 4 i + l / 16, 256 contiguous bytes per row (a load with one row per lane
+  // would touch 64 rows, 16 bytes each), and restage() passes the tile through the wave's own LDS rows into the
+  // one-row-per-lane layout. Other tiles load that layout directly, 4 bytes at a time.
+  constexpr int EV_RS = BN + 4;  // padded LDS row, floats: consecutive rows 4 banks apart
+  __shared__ __attribute__((aligned(16))) float Es[kThreads / 64][32 * EV_RS];
+  const float* ebase = p.er + b * p.er_sb + h * p.er_sh;
+  auto whole = [&](int t) { return VEC && (t + 1) * BN <= p.Sk; };
   auto load_ev = [&](int t, f32x4 (&dst)[NMB][4]) {
     const int kb = t * BN;
-    const bool whole = VEC && kb + BN <= p.Sk;  // 16-byte loads: every key of the tile exists
+    if (whole(t)) {
+#pragma unroll
+      for (int i = 0; i < 2 * NMB * 2; ++i) {
+        const int row = min(q0 + 32 * w + 4 * i + (lane >> 4), p.Sq - 1);
+        dst[i >> 2][i & 3] = *reinterpret_cast<const f32x4*>(ebase + (int64_t)row * p.er_ss + kb + 4 * (lane & 15));
+      }
+      return;
+    }
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
       for (int jq = 0; jq < 4; ++jq) {
         const int key = kb + mb * 32 + 8 * jq + 4 * g;
-        if (whole) {
-          dst[mb][jq] = *reinterpret_cast<const f32x4*>(erow + key);
-        } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) dst[mb][jq][e] = erow[min(key + e, p.Sk - 1)];
-        }
+        for (int e = 0; e < 4; ++e) dst[mb][jq][e] = erow[min(key + e, p.Sk - 1)];
       }
+  };
+  static_assert(NMB * 4 * 4 * 64 == 32 * BN * 4 / 4, "one wave's exp_rand tile: 8 16-byte loads per lane");
+  auto restage = [&](f32x4 (&x)[NMB][4]) {
+    float* ew = Es[w];
+#pragma unroll
+    for (int i = 0; i < 2 * NMB * 2; ++i)
+      *reinterpret_cast<f32x4*>(ew + (4 * i + (lane >> 4)) * EV_RS + 4 * (lane & 15)) = x[i >> 2][i & 3];
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq)
+        x[mb][jq] = *reinterpret_cast<const f32x4*>(ew + r * EV_RS + mb * 32 + 8 * jq + 4 * g);
   };
   auto tile = [&](int t, int buf, auto masked) {
     const int kb = t * BN;
+    if (whole(t)) restage(ev);
     f32x16 sacc[NMB];
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb) sacc[mb] = f32x16{};

@@ -319,10 +319,11 @@ def test_h2o_matches_oracle(gpu, S, H, D, sinks, dtype):
     np.testing.assert_array_equal(A.topk_indices(ref_cs.to(gpu), kk).cpu().numpy(), osel.topk_indices(ref_cs.numpy(), kk))
 
 
-def _colsum_reference(q, k, causal, softcap, window):
+def _colsum_reference(q, k, causal, softcap, window, power=1):
     """Column sums of the reference's probabilities (scores rounded in the input dtype as attn.py:29 and
     gemma2.py:29-33 round them, fp32 softmax, masked pairs -inf, rows that see no key contributing nothing), per
-    query head, summed in float64. GQA: query head h reads KV head h // (Hq / Hkv)."""
+    query head, summed in float64; power=2 sums their squares (roco.py:43-47). GQA: query head h reads KV head
+    h // (Hq / Hkv)."""
     B, Sq, Hq, D = q.shape
     Sk, Hkv = k.shape[1], k.shape[2]
     qt = q.transpose(1, 2)
@@ -334,7 +335,7 @@ def _colsum_reference(q, k, causal, softcap, window):
         m = oa._mask(i0, n, Sq, Sk, causal, window or None)
         if m is not None:
             s = s.masked_fill(m, float("-inf"))
-        total += torch.softmax(s, -1).nan_to_num(0.0).double().sum(2)
+        total += (torch.softmax(s, -1).nan_to_num(0.0).double() ** power).sum(2)
     return total
 
 
@@ -366,6 +367,27 @@ def test_colsum_variants(gpu, D, Sq, Sk, causal, window, softcap, dtype, base2):
     cs = A.attention_colsum(q.to(gpu), k.to(gpu), lse, ref_rounding=False, **kw).cpu()
     ref = _colsum_reference(q.float(), k.float(), causal, softcap, window).float()
     assert_close(cs, ref, 1e-3, 1e-2, what + " fp32 scores vs fp32 reference")
+
+
+@pytest.mark.parametrize("Sq,Sk,Hq,Hkv,causal,window,dtype", [
+    (256, 256, 4, 2, False, 0, torch.float16),     # exactly two mask-free query tiles: the shortest pipelined run
+    (900, 1100, 4, 4, True, 500, torch.float16),   # window, Sq < Sk, ragged ends
+    (1030, 1030, 4, 2, True, 0, torch.bfloat16),   # GQA, ragged last query tile
+])
+def test_colscore_sum_and_sumsq_variants(gpu, Sq, Sk, Hq, Hkv, causal, window, dtype):
+    # RoCo's epilogue (sums of p and p^2, roco.py:43-47) through the column-score primitive on the shapes the
+    # software-pipelined column pass meets besides the causal square case: no mask, a window, GQA, ragged tiles
+    from deepgengraph_amd import _lib
+
+    D = 128
+    q, k, v = _qkv(1, Sq, Sk, Hq, Hkv, D, dtype, 91 + Sq + Sk)
+    kw = dict(causal=causal, window=window)
+    what = f"colscore sum/sumsq Sq{Sq} Sk{Sk} H{Hq}/{Hkv} causal{causal} w{window} {dtype}"
+    _, lse = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), return_lse=True, ref_rounding=True, lse_base2=True, **kw)
+    s1, s2 = A.attention_colscore(q.to(gpu), k.to(gpu), lse, epilogue=_lib.COL_SUM_SQ, ref_rounding=True,
+                                  lse_base2=True, **kw)
+    _colsum_check(s1.cpu(), _colsum_reference(q, k, causal, 0.0, window).float(), what + " sum")
+    _colsum_check(s2.cpu(), _colsum_reference(q, k, causal, 0.0, window, power=2).float(), what + " sum of squares")
 
 
 def test_column_wrappers_reject_mismatched_k(gpu):

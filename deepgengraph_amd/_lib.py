@@ -15,6 +15,9 @@ import torch
 # DGG_LIBRARY overrides the in-tree library path (e.g. to compare builds).
 LIB_PATH = Path(os.environ.get("DGG_LIBRARY", Path(__file__).resolve().parent / "libdgg_hip.so"))
 
+# The ABI version of include/dgg.h this binding is written against; a library reporting another is refused.
+ABI_VERSION = 2
+
 DGG_F32, DGG_F16, DGG_BF16 = 0, 1, 2
 ATTN_CAUSAL = 0x1
 ATTN_REF_ROUNDING = 0x2
@@ -87,9 +90,14 @@ def load() -> ctypes.CDLL:
         except OSError as e:
             raise RuntimeError(f"failed to load {LIB_PATH}: {e}") from e
         for name, (res, args) in SIGNATURES.items():
-            fn = getattr(lib, name)
+            fn = getattr(lib, name, None)
+            if fn is None:
+                raise RuntimeError(f"{LIB_PATH} does not export {name}: rebuild it with `python -m deepgengraph_amd.build`")
             fn.restype = res
             fn.argtypes = args
+        version = lib.dgg_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} reports ABI version {version}, this binding expects {ABI_VERSION}: rebuild it")
         _lib = lib
         return lib
 

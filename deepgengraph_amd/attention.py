@@ -64,6 +64,35 @@ def rotary_cos_sin(positions: torch.Tensor, head_dim: int, rope_theta: float) ->
     return out
 
 
+def _tag_lse(lse: torch.Tensor, ref_rounding: bool, lse_base2: bool) -> torch.Tensor:
+    """Records on an lse tensor the options of the forward that wrote it, so that the column passes can take them
+    from it (a copy or a slice of the tensor does not carry them)."""
+    lse.dgg_ref_rounding = bool(ref_rounding)
+    lse.dgg_lse_base2 = bool(lse_base2)
+    return lse
+
+
+def _lse_options(name: str, lse: torch.Tensor, ref_rounding, lse_base2):
+    """The (ref_rounding, lse_base2) a column pass must use with `lse`: the scores must be rounded as the forward
+    that wrote the lse rounded them, and the lse read in the base it was written in. Values not given are taken from
+    the record attention() leaves on its lse; a given value that contradicts the record is refused, and so is a
+    missing ref_rounding for an lse without a record."""
+    tag_rr = getattr(lse, "dgg_ref_rounding", None)
+    tag_b2 = getattr(lse, "dgg_lse_base2", None)
+    if ref_rounding is None:
+        if tag_rr is None:
+            raise RuntimeError(f"{name}: pass ref_rounding= as given to the attention() call that wrote lse (this lse "
+                               "tensor carries no record of it)")
+        ref_rounding = tag_rr
+    elif tag_rr is not None and bool(ref_rounding) != tag_rr:
+        raise RuntimeError(f"{name}: ref_rounding={bool(ref_rounding)} but lse was written with ref_rounding={tag_rr}")
+    if lse_base2 is None:
+        lse_base2 = bool(tag_b2) if tag_b2 is not None else False
+    elif tag_b2 is not None and bool(lse_base2) != tag_b2:
+        raise RuntimeError(f"{name}: lse_base2={bool(lse_base2)} but lse was written with lse_base2={tag_b2}")
+    return bool(ref_rounding), bool(lse_base2)
+
+
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool = True, softcap: float = 0.0,
               window: int = 0, scale: float | None = None, return_lse: bool = False, ref_rounding: bool = False,
               out: torch.Tensor | None = None, lse_base2: bool = False, rope_cos_sin: torch.Tensor | None = None):
@@ -96,7 +125,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool
         _check_bshd("out", out)
         if out.shape != q.shape or out.dtype != q.dtype:
             raise RuntimeError("attention: out must match q in shape and dtype")
-    lse = torch.empty(B, Hq, Sq, dtype=torch.float32, device=q.device) if return_lse else None
+    lse = _tag_lse(torch.empty(B, Hq, Sq, dtype=torch.float32, device=q.device), ref_rounding,
+                   lse_base2) if return_lse else None
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
     if rope_cos_sin is not None:
         if (rope_cos_sin.dtype != torch.float32 or not rope_cos_sin.is_contiguous()
@@ -134,14 +164,17 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool
 
 def attention_colsum(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor, *, causal: bool = True,
                      softcap: float = 0.0, window: int = 0, scale: float | None = None,
-                     ref_rounding: bool = True, lse_base2: bool = False) -> torch.Tensor:
+                     ref_rounding: bool | None = None, lse_base2: bool | None = None) -> torch.Tensor:
     """Column sums of the softmax probabilities over the query axis, per query head: [B, Hq, Sk] fp32, recomputed
-    from q, k and the lse written by attention(..., return_lse=True) with the same options (ref_rounding and
-    lse_base2 included). ref_rounding (the default) rounds the 16-bit scores where the reference's eager module
-    rounds them (attn.py:29, gemma2.py:29-33), which the selection cases' 1e-3 contract on the sums needs;
-    ref_rounding=False keeps fp32 scores (faster, but up to ~1% off the reference's sums in 16-bit)."""
+    from q, k and the lse written by attention(..., return_lse=True) with the same options. ref_rounding and
+    lse_base2 must be those of that call: left as None they are read from the record attention() keeps on its lse,
+    and a value that contradicts the record raises (for an lse without the record, ref_rounding must be given).
+    ref_rounding=True rounds the 16-bit scores where the reference's eager module rounds them (attn.py:29,
+    gemma2.py:29-33), which the selection cases' 1e-3 contract on the sums needs; False keeps fp32 scores (faster,
+    but up to ~1% off the reference's sums in 16-bit)."""
     dev = _lib.require_gpu(q, k, lse)
     _check_qk("attention_colsum", q, k)
+    ref_rounding, lse_base2 = _lse_options("attention_colsum", lse, ref_rounding, lse_base2)
     B, Sq, Hq, D = q.shape
     Sk, Hkv = k.shape[1], k.shape[2]
     if lse.shape != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
@@ -172,13 +205,15 @@ def h2o_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, ref_roun
 
 def attention_colscore(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor, *, epilogue: int,
                        thr: torch.Tensor | None = None, causal: bool = True, window: int = 0,
-                       scale: float | None = None, ref_rounding: bool = True, lse_base2: bool = False):
-    """Column scores over the query axis from q, k and the forward's lse (same options, ref_rounding included: see
-    attention_colsum), per query head [B, Hq, Sk]:
+                       scale: float | None = None, ref_rounding: bool | None = None,
+                       lse_base2: bool | None = None):
+    """Column scores over the query axis from q, k and the forward's lse (same options; ref_rounding and lse_base2
+    as in attention_colsum), per query head [B, Hq, Sk]:
     epilogue COL_SUM -> sum_i p; COL_SUM_SQ -> (sum_i p, sum_i p^2) (roco.py:43-47); COL_ANY_GE -> bool
     any_i p[i, j] >= thr[i, j] with thr fp32 [Sq, Sk] (corm.py:35-37)."""
     dev = _lib.require_gpu(q, k, lse, thr)
     _check_qk("attention_colscore", q, k)
+    ref_rounding, lse_base2 = _lse_options("attention_colscore", lse, ref_rounding, lse_base2)
     B, Sq, Hq, D = q.shape
     Sk, Hkv = k.shape[1], k.shape[2]
     if lse.shape != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():

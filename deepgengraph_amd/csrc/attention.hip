@@ -392,7 +392,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
         for (int e = 0; e < 4; ++e) dst[mb][jq][e] = erow[min(key + e, p.Sk - 1)];
       }
   };
-  static_assert(NMB * 4 * 4 * 64 == 32 * BN * 4 / 4, "one wave's exp_rand tile: 8 16-byte loads per lane");
+  // The coalesced addressing above (load i: row 4i + lane/16, keys 4*(lane%16)..+3) covers exactly the wave's 32 rows
+  // by 64 keys: 2*NMB*2 loads of 4 rows, 16 lanes x 4 keys per row.
+  static_assert(BN == 64 && 16 * 4 == BN && 4 * (2 * NMB * 2) == 32, "coalesced exp_rand layout assumes 64-key tiles");
   auto restage = [&](f32x4 (&x)[NMB][4]) {
     float* ew = Es[w];
 #pragma unroll

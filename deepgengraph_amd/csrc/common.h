@@ -23,6 +23,14 @@ inline int dtype_size(int dtype) { return dtype == DGG_F32 ? 4 : 2; }
 inline bool valid_dtype(int dtype) { return dtype == DGG_F32 || dtype == DGG_F16 || dtype == DGG_BF16; }
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Decode (decode.hip): validates the arguments of a dgg_attn_decode call and launches it with the split partials in
+// `workspace`. With resolve_ws (the allocation-free entry point, decode_noalloc.hip), workspace_bytes is the size of
+// a fixed buffer that resolve_ws supplies once the arguments are valid.
+int decode_launch(const char* op, const void* q, const void* k, const void* v, void* o, float* lse, void* workspace,
+                  int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
+                  const int64_t* strides, int64_t splits, float scale, int dtype, void* stream,
+                  int (*resolve_ws)(const char* op, void* stream, void** ws));
+
 }  // namespace dgg
 
 #define DGG_REQUIRE(cond, code, ...)            \

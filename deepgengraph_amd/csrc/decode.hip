@@ -8,7 +8,6 @@
 // merged once through LDS into the split's partial (unnormalised output, max, sum) in the workspace.
 // A second small kernel merges the splits of each (batch, head).
 #include <algorithm>
-#include <mutex>
 
 #include "common.h"
 
@@ -172,54 +171,14 @@ extern "C" int64_t dgg_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_
   return B * Hq * splits * (D + 2) * (int64_t)sizeof(float);
 }
 
-namespace {
+namespace dgg {
 
-// ------------------------------------------------------------------------------------------------
-// Allocation-free decode. The split partials live in `scratch`, a file-scope device array of
-// kDecodeScratchBytes that every GPU the library runs on holds until the process ends. Host code never passes
-// the array's name to a kernel (on the host it is only a stand-in for the symbol): the device address is looked
-// up once per device with hipGetSymbolAddress and cached. The partial kernel writes every (batch, head, split)
-// entry before the merge reads it, so nothing needs clearing between calls; calls that overlap on one GPU share
-// the array and race.
-// ------------------------------------------------------------------------------------------------
-constexpr int64_t kDecodeScratchBytes = 96ll << 20;
-static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
-
-constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
-
-// Device address of this device's `scratch`, for the device the stream runs on (which must be current).
-int device_scratch(const char* op, void* stream, void** out) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
-  DGG_REQUIRE(e == hipSuccess, DGG_ERR_LAUNCH, "%s: hipGetDevice failed: %s", op, hipGetErrorString(e));
-  DGG_REQUIRE(dev >= 0 && dev < kMaxDevices, DGG_ERR_LAUNCH, "%s: device %d out of range", op, dev);
-  if (stream != nullptr) {
-    int sdev = -1;
-    e = hipStreamGetDevice(dgg::as_stream(stream), &sdev);
-    DGG_REQUIRE(e == hipSuccess, DGG_ERR_LAUNCH, "%s: hipStreamGetDevice failed: %s", op, hipGetErrorString(e));
-    DGG_REQUIRE(sdev == dev, DGG_ERR_LAUNCH, "%s: the stream belongs to device %d but device %d is current", op, sdev,
-                dev);
-  }
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (g_scratch_ptr[dev] == nullptr) {
-    void* ptr = nullptr;
-    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    DGG_REQUIRE(e == hipSuccess && ptr != nullptr, DGG_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed: %s", op,
-                hipGetErrorString(e));
-    g_scratch_ptr[dev] = ptr;
-  }
-  *out = g_scratch_ptr[dev];
-  return DGG_OK;
-}
-
-// Shared body of dgg_attn_decode and dgg_attn_decode_noalloc: validates every argument, then launches the
-// partial and merge kernels with the partials in `workspace` (use_scratch: in this device's `scratch` instead,
-// workspace_bytes being its fixed size).
-int decode_impl(const char* op, const void* q, const void* k, const void* v, void* o, float* lse, void* workspace,
-                int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
-                const int64_t* strides, int64_t splits, float scale, int dtype, void* stream, bool use_scratch) {
+// Shared body of dgg_attn_decode and dgg_attn_decode_noalloc (declared in common.h).
+int decode_launch(const char* op, const void* q, const void* k, const void* v, void* o, float* lse, void* workspace,
+                  int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
+                  const int64_t* strides, int64_t splits, float scale, int dtype, void* stream,
+                  int (*resolve_ws)(const char* op, void* stream, void** ws)) {
+  const bool use_scratch = resolve_ws != nullptr;
   DGG_REQUIRE(dtype == DGG_F16 || dtype == DGG_BF16, DGG_ERR_DTYPE,
               "%s: dtype code %d not supported (attention kernels take f16 or bf16)", op, dtype);
   DGG_REQUIRE(D == 64 || D == 128 || D == 256, DGG_ERR_UNSUPPORTED, "%s: head_dim %lld not supported (64, 128, 256)",
@@ -246,7 +205,7 @@ int decode_impl(const char* op, const void* q, const void* k, const void* v, voi
   if (B == 0) return DGG_OK;
   DGG_REQUIRE(q && k && v && o, DGG_ERR_NULL, "%s: null pointer", op);
   if (use_scratch) {
-    if (int rc = device_scratch(op, stream, &workspace)) return rc;
+    if (int rc = resolve_ws(op, stream, &workspace)) return rc;
   }
   DGG_REQUIRE(workspace != nullptr, DGG_ERR_NULL, "%s: null workspace", op);
   DGG_REQUIRE(dgg::aligned16(q) && dgg::aligned16(k) && dgg::aligned16(v) && dgg::aligned16(workspace),
@@ -284,18 +243,11 @@ int decode_impl(const char* op, const void* q, const void* k, const void* v, voi
   return dgg::check_launch(op);
 }
 
-}  // namespace
+}  // namespace dgg
 
 extern "C" int dgg_attn_decode(const void* q, const void* k, const void* v, void* o, float* lse, void* workspace,
                                int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
                                const int64_t* strides, int64_t splits, float scale, int dtype, void* stream) {
-  return decode_impl("attn_decode", q, k, v, o, lse, workspace, workspace_bytes, B, Hq, Hkv, L, D, strides, splits,
-                     scale, dtype, stream, false);
-}
-
-extern "C" int dgg_attn_decode_noalloc(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B,
-                                       int64_t Hq, int64_t Hkv, int64_t L, int64_t D, const int64_t* strides,
-                                       int64_t splits, float scale, int dtype, void* stream) {
-  return decode_impl("attn_decode_noalloc", q, k, v, o, lse, nullptr, kDecodeScratchBytes, B, Hq, Hkv, L, D, strides,
-                     splits, scale, dtype, stream, true);
+  return dgg::decode_launch("attn_decode", q, k, v, o, lse, workspace, workspace_bytes, B, Hq, Hkv, L, D, strides,
+                            splits, scale, dtype, stream, nullptr);
 }

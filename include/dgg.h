@@ -21,7 +21,9 @@
 extern "C" {
 #endif
 
-#define DGG_ABI_VERSION 1
+/* 2: dgg_ref_multiplier removed; DGG_ATTN_REF_ROUNDING divides as torch does on the GPU (multiply by the fp32
+ * reciprocal); top-k ranks NaN above +inf; the split-KV entry points (dgg_attn_splitkv*) added. */
+#define DGG_ABI_VERSION 2
 
 enum dgg_dtype { DGG_F32 = 0, DGG_F16 = 1, DGG_BF16 = 2 };
 

@@ -43,7 +43,7 @@ def test_header_and_binding_agree(lib):
 
 
 def test_version_and_error_string(lib):
-    assert lib.dgg_abi_version() == 1
+    assert lib.dgg_abi_version() == _lib.ABI_VERSION == 2
     assert isinstance(lib.dgg_last_error(), bytes)
 
 
@@ -236,3 +236,26 @@ def test_python_wrappers_reject_cpu_tensors():
     q = torch.zeros(1, 8, 2, 64, dtype=torch.float16)
     with pytest.raises(RuntimeError, match="GPU tensor"):
         attention.attention(q, q, q)
+
+
+def test_column_pass_options_follow_the_lse_record():
+    # the column passes take ref_rounding / lse_base2 from the record attention() keeps on its lse, refuse a value
+    # that contradicts it, and need ref_rounding for an lse without one (host logic only: no launch)
+    import torch
+
+    from deepgengraph_amd import attention as A
+
+    lse = torch.zeros(1, 2, 8)
+    with pytest.raises(RuntimeError, match="carries no record"):
+        A._lse_options("colsum", lse, None, None)
+    assert A._lse_options("colsum", lse, True, None) == (True, False)
+    assert A._lse_options("colsum", lse, False, True) == (False, True)
+    for rr in (False, True):
+        for b2 in (False, True):
+            tagged = A._tag_lse(torch.zeros(1, 2, 8), rr, b2)
+            assert A._lse_options("colsum", tagged, None, None) == (rr, b2)
+            assert A._lse_options("colsum", tagged, rr, b2) == (rr, b2)
+            with pytest.raises(RuntimeError, match="ref_rounding"):
+                A._lse_options("colsum", tagged, not rr, None)
+            with pytest.raises(RuntimeError, match="lse_base2"):
+                A._lse_options("colsum", tagged, None, not b2)

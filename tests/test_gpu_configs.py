@@ -1,6 +1,6 @@
 """Full-size parity for the five benchmark configurations (deepgengraph_amd.configs) on identical seeded inputs.
-Where the CPU oracle would take minutes at full size, a documented subset is checked against it (whole heads
-over the full sequence) and size-independent properties cover the rest."""
+Every head of every configuration is checked against the CPU oracle at full size; config 5's 34 GB cache comes to
+the host one batch entry at a time."""
 import math
 
 import numpy as np
@@ -38,17 +38,18 @@ def test_config2_block_full(gpu):
     assert_close(out.cpu().float(), ref.float(), 2e-2, 1e-2, "config 2 block output")
 
 
-def test_config3_gemma2_full_sequences(gpu):
+def test_config3_gemma2_full(gpu):
     cfg = C.CFG3
     q, k, v, _ = C.attn_inputs(cfg)
     out = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), causal=True, softcap=cfg.softcap, window=cfg.window).cpu()
-    # whole sequences of (batch 0, head 0), (batch 1, head 5), (batch 1, head 15): every query row, all 8192 keys
-    for b, h in ((0, 0), (1, 5), (1, 15)):
-        hk = h // (cfg.Hq // cfg.Hkv)
-        ref = oa.attention(q[b:b + 1, :, h:h + 1], k[b:b + 1, :, hk:hk + 1], v[b:b + 1, :, hk:hk + 1], causal=True,
-                           softcap=cfg.softcap, window=cfg.window)
-        assert_close(out[b:b + 1, :, h:h + 1].float(), ref.float(), 2e-2, 1e-2, f"config 3 b{b} h{h}")
-    assert torch.isfinite(out.float()).all()
+    progress("config 3: GPU done")
+    # every (batch, head) sequence: all 8192 query rows against all 8192 keys
+    ref = oa.attention(q, k, v, causal=True, softcap=cfg.softcap, window=cfg.window)
+    progress("config 3: oracle done")
+    for b in range(cfg.B):
+        for h in range(cfg.Hq):
+            assert_close(out[b:b + 1, :, h:h + 1].float(), ref[b:b + 1, :, h:h + 1].float(), 2e-2, 1e-2,
+                         f"config 3 b{b} h{h}")
 
 
 def test_config4_h2o_full(gpu):
@@ -60,27 +61,35 @@ def test_config4_h2o_full(gpu):
     progress("config 4: GPU done")
     assert_close(csc.sum(-1), torch.full((1, cfg.Hq), float(cfg.Sq)), 0, 1e-4, "sum of colsums (all heads)")
     assert (np.diff(idx, axis=-1) > 0).all(), "indices ascending and distinct"
-    # oracle on whole heads (all 4096 queries and keys), 4 of the 32 heads
-    for h in (0, 11, 22, 31):
-        ref_out, ref_cs, _ = oa.h2o(q[:, :, h:h + 1], k[:, :, h:h + 1], v[:, :, h:h + 1])
-        progress(f"config 4: oracle head {h} done")
-        assert_close(out[:, :, h:h + 1].float(), ref_out.float(), 1e-2, 5e-3, f"config 4 out head {h}")
-        assert_close(csc[:, h:h + 1], ref_cs, 1e-6, 1e-3, f"config 4 colsum head {h}")
-        np.testing.assert_array_equal(idx[:, h:h + 1], osel.topk_indices(ref_cs.numpy(), cfg.topk))
+    # oracle on every head: all 4096 queries and keys
+    ref_out, ref_cs, _ = oa.h2o(q, k, v)
+    ref_idx = osel.topk_indices(ref_cs.numpy(), cfg.topk)
+    progress("config 4: oracle done")
+    for h in range(cfg.Hq):
+        assert_close(out[:, :, h:h + 1].float(), ref_out[:, :, h:h + 1].float(), 1e-2, 5e-3, f"config 4 out head {h}")
+        assert_close(csc[:, h:h + 1], ref_cs[:, h:h + 1], 1e-6, 1e-3, f"config 4 colsum head {h}")
+        np.testing.assert_array_equal(idx[:, h], ref_idx[:, h], err_msg=f"config 4 top-256 head {h}")
 
 
+@pytest.mark.timeout(600)
 def test_config5_decode_full(gpu):
     cfg = C.CFG5
     q, kc, vc = C.decode_inputs(cfg, device=gpu)
     progress("config 5: cache generated")
     out, lse = A.decode_attention(q, kc, vc, splits=cfg.splits, return_lse=True)
-    torch.cuda.synchronize()
-    assert torch.isfinite(out.float()).all()
-    for b, h in ((0, 0), (17, 5), (40, 31), (63, 31)):
-        ref, ref_lse = oa.decode(q[b:b + 1, h:h + 1].cpu(), kc[b:b + 1, h:h + 1].cpu(), vc[b:b + 1, h:h + 1].cpu())
-        assert_close(out[b:b + 1, h:h + 1].cpu().float(), ref.float(), 1e-2, 5e-3, f"config 5 decode b{b} h{h}")
-        assert_close(lse[b:b + 1, h:h + 1].cpu(), ref_lse, 1e-3, 1e-4, f"config 5 lse b{b} h{h}")
+    out, lse, qc = out.cpu(), lse.cpu(), q.cpu()
+    # every batch entry and head: one batch's K / V slice (537 MB) comes to the host at a time
+    for b in range(cfg.B):
+        ref, ref_lse = oa.decode(qc[b:b + 1], kc[b:b + 1].cpu(), vc[b:b + 1].cpu())
+        assert_close(out[b:b + 1].float(), ref.float(), 1e-2, 5e-3, f"config 5 decode batch {b}")
+        assert_close(lse[b:b + 1], ref_lse, 1e-3, 1e-4, f"config 5 lse batch {b}")
+        if b % 16 == 15:
+            progress(f"config 5: batches 0-{b} checked")
     del kc, vc
+
+
+def test_config5_prestep(gpu):
+    cfg = C.CFG5
     pre = C.decode_prestep_inputs(cfg)
     normed, act = decode_prestep(*(pre[n].to(gpu) for n in ("x", "w_norm", "gate_up")), eps=C.LLAMA_EPS)
     assert_close(normed.cpu().float(), oe.rms_norm(pre["x"], pre["w_norm"], C.LLAMA_EPS).float(), 1e-2, 5e-3,

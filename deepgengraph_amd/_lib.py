@@ -65,6 +65,9 @@ SIGNATURES = {
     "dgg_attn_decode_noalloc": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64p, _i64, _f32, _i32,
                                        _vp]),
     "dgg_attn_decode_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
+    "dgg_attn_splitkv_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "dgg_attn_splitkv": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64p, _i64,
+                                _f32, _f32, _i64, _u32, _i32, _vp]),
     "dgg_attn_decode": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64p, _i64, _f32,
                                _i32, _vp]),
 }

@@ -43,6 +43,33 @@ def _decode_shaped(Sq: int, Sk: int, softcap, window, ref_rounding: bool, dtype)
             and dtype in (torch.float16, torch.bfloat16))
 
 
+# Short query blocks over long key ranges (chunked prefill, multi-row and grouped-query decode) run on the split-KV
+# kernels: at most SPLITKV_MAX_QLEN query rows and SPLITKV_MAX_ROWS rows per KV head (query heads of the group x
+# query rows), over at least SPLITKV_MIN_KEYS keys. The prefill kernel would give each (batch, head) one workgroup
+# of 256 rows, mostly empty, and read the whole key range in it.
+SPLITKV_MAX_QLEN = 64
+SPLITKV_MAX_ROWS = 128
+SPLITKV_MIN_KEYS = 512
+
+
+def _splitkv_shaped(Sq: int, Sk: int, Hq: int, Hkv: int, ref_rounding: bool, dtype) -> bool:
+    rows = (Hq // Hkv) * Sq
+    return (Sq <= SPLITKV_MAX_QLEN and rows <= SPLITKV_MAX_ROWS and Sk >= SPLITKV_MIN_KEYS and Sk >= 4 * Sq
+            and not ref_rounding and dtype in (torch.float16, torch.bfloat16))
+
+
+def splitkv_splits(B: int, Sq: int, Hq: int, Hkv: int, span: int) -> int:
+    """Key slices for a split-KV call over `span` keys: about 4096 workgroups over the chip, each slice at least 256
+    keys and at least 32 keys per row it serves (so the partials written and merged stay a few percent of the K / V
+    bytes read)."""
+    rows = (Hq // Hkv) * Sq
+    rpw = 32 if rows <= 32 else 64
+    groups = B * Hkv * (-(-rows // rpw))
+    want = -(-4096 // max(1, groups))
+    min_keys = max(256, 32 * min(rows, rpw))
+    return int(max(1, min(1024, want, -(-span // min_keys))))
+
+
 def decode_splits(B: int, Hq: int, L: int) -> int:
     """Split count for a decode call: at least ~2048 workgroups over the chip (8 per CU) when the cache allows,
     and at least 128 keys per split (one unrolled block of the partial kernel)."""
@@ -104,8 +131,10 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool
     gemma2.py:19-38): scores = q.k^T * scale (default 1/sqrt(D)), optional softcap*tanh(scores/softcap),
     bottom-right aligned causal mask (attn.py:22-23), optional sliding window (key j visible iff
     i + Sk - Sq - j < window), fp32 softmax, P.V. ref_rounding rounds the scores to the input dtype at the
-    reference's rounding points (slower; used for H2O selection parity). A one-row call over at least
-    DECODE_MIN_KEYS keys (the reference's decode case) runs on the split-KV decode kernels.
+    reference's rounding points (slower; used for H2O selection parity). A one-row multi-head call over at least
+    DECODE_MIN_KEYS keys (the reference's decode case) runs on the split-KV decode kernels; other short query blocks
+    over long key ranges (_splitkv_shaped: chunked prefill, multi-row and grouped-query decode) on the split-KV
+    attention kernels (splitkv_attention).
 
     rope_cos_sin (head_dim 128, 16-bit inputs): q is taken unrotated and each query row is rotated inside the
     kernel by its row of this table (rotary_cos_sin of the rows' positions, [B * Sq, 128], batch-major), as
@@ -139,7 +168,7 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool
                   Sk, Hq, Hkv, D, strides, scale, float(softcap or 0.0), int(window or 0), flags,
                   _lib.dtype_code(q.dtype), _lib.ptr(rope_cos_sin), _lib.stream_handle(dev))
         return (out, lse) if return_lse else out
-    if _decode_shaped(Sq, Sk, softcap, window, ref_rounding, q.dtype):
+    if Hq == Hkv and _decode_shaped(Sq, Sk, softcap, window, ref_rounding, q.dtype):
         # One query row (attn.py:22-23: the bottom-right causal mask hides nothing): the split-KV decode kernels,
         # reading the case layout [B, L, H, D] through its strides.
         splits = decode_splits(B, Hq, Sk)
@@ -153,12 +182,56 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool
         if return_lse:
             lse.copy_(lse1.view(B, Hq, 1) * (math.log2(math.e) if lse_base2 else 1.0))
         return (out, lse) if return_lse else out
+    if _splitkv_shaped(Sq, Sk, Hq, Hkv, ref_rounding, q.dtype):
+        _splitkv(q, k, v, out, lse, causal, softcap, window, scale, lse_base2, None, dev)
+        return (out, lse) if return_lse else out
     flags = ((_lib.ATTN_CAUSAL if causal else 0) | (_lib.ATTN_REF_ROUNDING if ref_rounding else 0)
              | (_lib.ATTN_LSE_BASE2 if lse_base2 else 0))
     strides = _lib.int64_array([*q.stride()[:3], *k.stride()[:3], *v.stride()[:3], *out.stride()[:3]])
     _lib.call("dgg_attn_prefill", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out), _lib.ptr(lse), B, Sq, Sk,
               Hq, Hkv, D, strides, scale, float(softcap or 0.0), int(window or 0), flags, _lib.dtype_code(q.dtype),
               _lib.stream_handle(dev))
+    return (out, lse) if return_lse else out
+
+
+def _splitkv(q, k, v, out, lse, causal, softcap, window, scale, lse_base2, splits, dev):
+    B, Sq, Hq, D = q.shape
+    Sk, Hkv = k.shape[1], k.shape[2]
+    if splits is None:
+        first = max(0, Sk - Sq - window + 1) if window else 0
+        splits = splitkv_splits(B, Sq, Hq, Hkv, Sk - first)
+    need = int(_lib.load().dgg_attn_splitkv_workspace_bytes(B, Sq, Hq, D, splits))
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
+    flags = (_lib.ATTN_CAUSAL if causal else 0) | (_lib.ATTN_LSE_BASE2 if lse_base2 else 0)
+    strides = _lib.int64_array([*q.stride()[:3], *k.stride()[:3], *v.stride()[:3], *out.stride()[:3]])
+    _lib.call("dgg_attn_splitkv", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(ws),
+              ws.numel(), B, Sq, Sk, Hq, Hkv, D, strides, int(splits), float(scale), float(softcap or 0.0),
+              int(window or 0), flags, _lib.dtype_code(q.dtype), _lib.stream_handle(dev))
+
+
+def splitkv_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool = True,
+                      softcap: float = 0.0, window: int = 0, scale: float | None = None, return_lse: bool = False,
+                      lse_base2: bool = False, splits: int | None = None, out: torch.Tensor | None = None):
+    """attention() on the split-KV kernels, whatever the shape (attention() picks them by itself for short query
+    blocks over long key ranges): the keys any row sees are cut into `splits` slices (default splitkv_splits),
+    each workgroup takes one slice and up to 64 rows of a KV head (its query heads times the query rows), and a merge
+    combines the slices. Same arguments, semantics and results as attention() without reference rounding."""
+    dev = _lib.require_gpu(q, k, v, out)
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _check_bshd(name, t)
+    B, Sq, Hq, D = q.shape
+    if k.shape[0] != B or v.shape != k.shape or k.shape[3] != D:
+        raise RuntimeError(f"splitkv_attention: incompatible shapes q {tuple(q.shape)} k {tuple(k.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise RuntimeError("splitkv_attention: q, k, v dtypes differ")
+    if out is None:
+        out = torch.empty(B, Sq, Hq, D, dtype=q.dtype, device=q.device)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise RuntimeError("splitkv_attention: out must match q")
+    lse = _tag_lse(torch.empty(B, Hq, Sq, dtype=torch.float32, device=q.device), False,
+                   lse_base2) if return_lse else None
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    _splitkv(q, k, v, out, lse, causal, softcap, window, scale, lse_base2, splits, dev)
     return (out, lse) if return_lse else out
 
 

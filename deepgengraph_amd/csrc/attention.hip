@@ -1664,6 +1664,10 @@ void pick_kf_rowlse(const AttnParams& p, bool ref, bool vec, hipStream_t st) {
   });
 }
 
+}  // namespace
+
+namespace dgg_attn {
+
 // Shared host-side validation of the attention arguments.
 int validate_attn(const char* op, const void* q, const void* k, int64_t B, int64_t Sq, int64_t Sk, int64_t Hq,
                   int64_t Hkv, int64_t D, const int64_t* strides, int nstrides, float scale, float softcap,
@@ -1734,7 +1738,7 @@ AttnParams make_params(const void* q, const void* k, const void* v, void* o, int
   return p;
 }
 
-}  // namespace
+}  // namespace dgg_attn
 
 namespace {
 // Shared body of dgg_attn_prefill and dgg_attn_prefill_rope (rope: rotate the query rows by the table rope_cs).

@@ -312,6 +312,14 @@ __device__ __forceinline__ float rowsum8(f16x8 v, float l) {
 }
 
 
+// Host-side validation of the attention arguments shared by the prefill, column and split-KV entry points
+// (nstrides strides, every third one a sequence stride), and the launch parameters they derive.
+int validate_attn(const char* op, const void* q, const void* k, int64_t B, int64_t Sq, int64_t Sk, int64_t Hq,
+                  int64_t Hkv, int64_t D, const int64_t* strides, int nstrides, float scale, float softcap,
+                  int64_t window, int dtype);
+AttnParams make_params(const void* q, const void* k, const void* v, void* o, int64_t B, int64_t Sq, int64_t Sk,
+                       int64_t Hq, int64_t Hkv, int64_t D, float scale, float softcap, int64_t window, uint32_t flags);
+
 // Software-pipelined head_dim-256 forward (attention_d256.hip) for 16-bit inputs without reference rounding:
 // 4 waves x 32 rows per workgroup (p.n_tiles counts 128-row query tiles).
 void launch_attn_d256_pipe(const AttnParams& p, bool bf16, hipStream_t st);

@@ -31,6 +31,13 @@ int decode_launch(const char* op, const void* q, const void* k, const void* v, v
                   const int64_t* strides, int64_t splits, float scale, int dtype, void* stream,
                   int (*resolve_ws)(const char* op, void* stream, void** ws));
 
+// Split-KV attention (splitkv.hip): validates the arguments of a dgg_attn_splitkv call and launches it with the split
+// partials in `workspace` (resolve_ws as for decode_launch). Grouped-query decode calls run through it.
+int splitkv_launch(const char* op, const void* q, const void* k, const void* v, void* o, float* lse, void* workspace,
+                   int64_t workspace_bytes, int64_t B, int64_t Sq, int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D,
+                   const int64_t* strides, int64_t splits, float scale, float softcap, int64_t window, uint32_t flags,
+                   int dtype, void* stream, int (*resolve_ws)(const char* op, void* stream, void** ws));
+
 }  // namespace dgg
 
 #define DGG_REQUIRE(cond, code, ...)            \

@@ -204,6 +204,15 @@ int decode_launch(const char* op, const void* q, const void* k, const void* v, v
                 (long long)workspace_bytes, (long long)need);
   if (B == 0) return DGG_OK;
   DGG_REQUIRE(q && k && v && o, DGG_ERR_NULL, "%s: null pointer", op);
+  if (Hq > Hkv) {
+    // Grouped query heads: the split-KV kernels take the G query heads of a KV head as the rows of one workgroup, so
+    // each cache row is read once, not once per query head. The cache [B, Hkv, L, D] is their [B, Sk, Hkv, D] with
+    // strides {b, l, h}; the partials have the same size.
+    const int64_t st12[12] = {strides[0], 0,          strides[1], strides[2], strides[4], strides[3],
+                              strides[5], strides[7], strides[6], strides[8], 0,          strides[9]};
+    return dgg::splitkv_launch(op, q, k, v, o, lse, workspace, workspace_bytes, B, 1, L, Hq, Hkv, D, st12, splits,
+                               scale, 0.f, 0, 0u, dtype, stream, resolve_ws);
+  }
   if (use_scratch) {
     if (int rc = resolve_ws(op, stream, &workspace)) return rc;
   }

@@ -226,6 +226,21 @@ int64_t dgg_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int64_
 int dgg_attn_decode(const void* q, const void* k, const void* v, void* o, float* lse, void* workspace,
                     int64_t workspace_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
                     const int64_t* strides, int64_t splits, float scale, int dtype, void* stream);
+/* Split-KV attention for a few query rows over a long key range. No kernel counterpart in the reference: it serves
+ * the compile() callable of Attn / Gemma2 (attn.py:18-34, gemma2.py:19-38) when 1 <= q_len << kv_len, as in chunked
+ * prefill, multi-row and speculative decode, and grouped-query decode. Semantics, layouts and the 12 strides are
+ * those of dgg_attn_prefill (bottom-right causal mask, window, soft-cap, GQA, DGG_ATTN_LSE_BASE2); the lse is
+ * written for every row. DGG_ATTN_REF_ROUNDING is not supported (DGG_ERR_UNSUPPORTED). The keys any row sees are cut
+ * into `splits` slices; one workgroup takes a slice and up to 64 of the G * Sq rows of a KV head (its G = Hq / Hkv
+ * query heads times the Sq query rows), so each K / V row is read once per 64 rows; a merge kernel combines the
+ * slices. workspace: dgg_attn_splitkv_workspace_bytes(B, Sq, Hq, D, splits) bytes, 16-byte aligned. f16 / bf16,
+ * Sq >= 1, Sk >= 1, splits in [1, 1024]. dgg_attn_decode and dgg_attn_decode_noalloc run grouped-query calls
+ * (Hq > Hkv) through these kernels with the same workspace size. */
+int64_t dgg_attn_splitkv_workspace_bytes(int64_t B, int64_t Sq, int64_t Hq, int64_t D, int64_t splits);
+int dgg_attn_splitkv(const void* q, const void* k, const void* v, void* o, float* lse, void* workspace,
+                     int64_t workspace_bytes, int64_t B, int64_t Sq, int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D,
+                     const int64_t* strides, int64_t splits, float scale, float softcap, int64_t window,
+                     uint32_t flags, int dtype, void* stream);
 /* dgg_attn_decode without a workspace argument, for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc); no counterpart in the reference. The split
  * partials live in a fixed 96 MiB (100663296-byte) device array that each GPU the library runs on holds until the

@@ -24,6 +24,15 @@ import numpy as np
 import torch
 
 
+def _mm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a @ b in a's dtype with fp32 accumulation and one rounding at the end, as the GPU's 16-bit GEMM computes the
+    reference's matmuls. fp16 goes through fp32 products explicitly: CPUs without native fp16 arithmetic otherwise
+    take minutes per config-4 head, and on CPUs with it (AVX512-FP16) torch's fp16 matmul gives the same bits."""
+    if a.dtype == torch.float16:
+        return torch.matmul(a.float(), b.float()).to(torch.float16)
+    return torch.matmul(a, b)
+
+
 def div_scalar(x: torch.Tensor, d: float) -> torch.Tensor:
     """x / d for a tensor x and a Python float d, as torch computes it on the GPU (the reference's
     `torch.matmul(q, k^T) / math.sqrt(D)`, attn.py:29, and `scores /= softcap`, gemma2.py:31): the divisor is
@@ -36,7 +45,7 @@ def div_scalar(x: torch.Tensor, d: float) -> torch.Tensor:
 def _scores(qt: torch.Tensor, kT: torch.Tensor, D: int, softcap=None) -> torch.Tensor:
     """attn.py:29 / gemma2.py:29-33 in the input dtype: the matmul result rounded, divided by sqrt(D) (rounded),
     and with a soft-cap: divided by it, tanh, multiplied by it, each rounded."""
-    scores = div_scalar(torch.matmul(qt, kT), math.sqrt(D))
+    scores = div_scalar(_mm(qt, kT), math.sqrt(D))
     if softcap:
         scores = div_scalar(scores, softcap)
         scores = torch.tanh(scores)
@@ -93,7 +102,7 @@ def attention(q, k, v, *, causal=True, softcap=None, window=None, return_lse=Fal
             scores = scores.masked_fill(hidden, float("-inf"))  # attn.py:30 (`scores += mask`)
         sf = scores.float()
         probs = torch.softmax(sf, dim=-1)  # attn.py:31
-        out[:, :, i0:i0 + n] = torch.matmul(probs.to(dt), vt)  # attn.py:32
+        out[:, :, i0:i0 + n] = _mm(probs.to(dt), vt)  # attn.py:32
         if return_lse:
             lse[:, :, i0:i0 + n] = torch.logsumexp(sf, dim=-1)
     out = out.transpose(1, 2).contiguous()  # attn.py:32-34
@@ -119,7 +128,7 @@ def h2o(q, k, v, *, q_chunk=256):
         scores = scores.masked_fill(_mask(i0, n, Sq, Sk, True, None), float("-inf"))  # h2o.py:30
         sf = scores.float()
         probs = torch.softmax(sf, dim=-1)  # h2o.py:31
-        out[:, :, i0:i0 + n] = torch.matmul(probs.to(dt), vt)  # h2o.py:32
+        out[:, :, i0:i0 + n] = _mm(probs.to(dt), vt)  # h2o.py:32
         colsum += probs.sum(dim=2)  # h2o.py:35-36
         lse[:, :, i0:i0 + n] = torch.logsumexp(sf, dim=-1)
     return out.transpose(1, 2).contiguous(), colsum, lse
@@ -145,7 +154,7 @@ def _causal_probs(q, k, v, q_chunk):
             scores = scores.masked_fill(_mask(i0, n, Sq, Sk, True, None), float("-inf"))
             sf = scores.float()
             probs = torch.softmax(sf, dim=-1)
-            out[:, :, i0:i0 + n] = torch.matmul(probs.to(dt), vt)
+            out[:, :, i0:i0 + n] = _mm(probs.to(dt), vt)
             lse[:, :, i0:i0 + n] = torch.logsumexp(sf, dim=-1)
             yield i0, n, probs
 
@@ -212,7 +221,7 @@ def keyformer(q, k, v, exp_rand, *, tau=1.5, q_chunk=256):
         scores = _scores(qt[:, :, i0:i0 + n], kT, D)  # kf.py:29
         scores = scores.masked_fill(_mask(i0, n, Sq, Sk, True, None), float("-inf"))  # kf.py:30
         probs = torch.softmax(scores.float(), dim=-1)  # kf.py:31
-        out[:, :, i0:i0 + n] = torch.matmul(probs.to(dt), vt)  # kf.py:32
+        out[:, :, i0:i0 + n] = _mm(probs.to(dt), vt)  # kf.py:32
         gumbels = -exp_rand[:, :, i0:i0 + n].log()  # kf.py:36-37
         pert = (scores.float() + gumbels) / tau  # kf.py:38
         score += torch.softmax(pert, dim=-1).sum(dim=2)  # kf.py:39-40
@@ -252,7 +261,7 @@ def decode(q, k_cache, v_cache):
         scores = _scores(q[b].unsqueeze(1), kb.transpose(-2, -1), D)  # [Hq, 1, L], attn.py:29
         sf = scores.float()
         probs = torch.softmax(sf, dim=-1)
-        out[b] = torch.matmul(probs.to(dt), vb).squeeze(1)
+        out[b] = _mm(probs.to(dt), vb).squeeze(1)
         lse[b] = torch.logsumexp(sf, dim=-1).squeeze(1)
     return out, lse
 

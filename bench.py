@@ -300,6 +300,46 @@ def bench_variants(args, dev):
     return res
 
 
+def bench_splitkv(args, dev):
+    """Short query blocks over a long cache (attn.py:18-34 with q_len 4 / 16 over 32K keys, as in chunked prefill
+    and speculative decode) and grouped-query decode (16 query heads over 8 KV heads, roco.py:25-27): each call runs
+    the split-KV kernels. Rate = algorithmic bytes (K and V read once, q and o) per call."""
+    from deepgengraph_amd import attention as A
+
+    res = {}
+    H, D, L = 32, 128, 32768
+    for Sq, dt in ((4, torch.float16), (16, torch.bfloat16)):
+        g = torch.Generator(device=dev).manual_seed(Sq)
+        q = torch.randn(1, Sq, H, D, generator=g, device=dev).to(dt)
+        k = torch.randn(1, L, H, D, generator=g, device=dev).to(dt)
+        v = torch.randn(1, L, H, D, generator=g, device=dev).to(dt)
+        out = torch.empty_like(q)
+        ms, info = _variant(lambda: A.attention(q, k, v, causal=True, out=out), 20)
+        nb = 2 * (2 * k.numel() + 2 * q.numel())
+        gbps = nb / (ms * 1e-3) / 1e9
+        res[f"qlen{Sq}_kv{L}_h{H}_d{D}"] = dict(us=round(ms * 1e3, 2), gbps=round(gbps, 1),
+                                                 frac=round(gbps / PEAK_HBM_GBPS, 4),
+                                                 splits=A.splitkv_splits(1, Sq, H, H, L), **info)
+        del q, k, v, out
+    B, Hq, Hkv = 64, 16, 8
+    g = torch.Generator(device=dev).manual_seed(7)
+    q = torch.randn(B, Hq, D, generator=g, device=dev).half()
+    kc = torch.randn(B, Hkv, L, D, generator=g, device=dev).half()
+    vc = torch.randn(B, Hkv, L, D, generator=g, device=dev).half()
+    splits = 64
+    ws = torch.empty(A.decode_workspace_bytes(B, Hq, D, splits), dtype=torch.uint8, device=dev)
+    out = torch.empty_like(q)
+    ms, info = _variant(lambda: A.decode_attention(q, kc, vc, splits=splits, out=out, workspace=ws), 10)
+    nb = 2 * (2 * kc.numel() + 2 * q.numel())
+    gbps = nb / (ms * 1e-3) / 1e9
+    res[f"gqa_decode_b{B}_h{Hq}/{Hkv}_kv{L}_d{D}_f16"] = dict(ms=round(ms, 4), gbps=round(gbps, 1),
+                                                             frac=round(gbps / PEAK_HBM_GBPS, 4), splits=splits,
+                                                             **info)
+    del q, kc, vc, ws, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_block(args, dev):
     from deepgengraph_amd import configs as C
     from deepgengraph_amd.llama import LlamaAttentionBlock
@@ -373,7 +413,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--sections", default="prefill,decode,prestep,variants,block")
+    ap.add_argument("--sections", default="prefill,decode,splitkv,prestep,variants,block")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-steady", action="store_true", help="skip the steady-clock figure (short profiled runs)")
     args = ap.parse_args()
@@ -391,6 +431,8 @@ def main():
     cfg = pre["cfg"]
     if "decode" in sections:
         extra["decode"] = bench_decode(args, dev)
+    if "splitkv" in sections:
+        extra["splitkv"] = bench_splitkv(args, dev)
     if "prestep" in sections:
         extra["elementwise"] = bench_prestep(args, dev)
     if "variants" in sections:

@@ -9,8 +9,8 @@
 // once per query head and row. Each split writes an unnormalised partial (O, row maximum, row sum) per row; a merge
 // kernel combines the splits of each row as the decode merge does.
 //
-// Tile loop. Keys in tiles of 32: the workgroup copies K and V rows global -> registers (coalesced 16-byte loads)
-// -> LDS (rows padded by 16 bytes), one tile ahead of the compute. Each wave then runs
+// Tile loop. Keys in tiles of 32: the workgroup copies K and V rows global -> registers (16-byte loads, consecutive
+// lanes on consecutive chunks of a row) -> LDS (rows padded by 16 bytes), one tile ahead of the compute. Each wave then runs
 //   S^T (32 keys x 32 rows) = K . Q^T     v_mfma_f32_32x32x16, A = K fragments from LDS, B = Q in registers
 //   O^T (D x 32 rows)      += V^T . P^T   A = V^T by transposing LDS reads, B = P straight from the S^T accumulator
 // with the online softmax of the prefill kernels (one query row per lane, the cross-half exchange, lazy rescale).
@@ -64,9 +64,10 @@ attn_splitkv_kernel(SplitParams sp) {
   constexpr int NDB = D / 32;           // 32-wide head-dim blocks of O^T
   constexpr int NPK = BN / 16;          // MFMA k-steps over the keys of a tile in P.V
   constexpr int NT = 64 * NW;
-  constexpr int CPT = BN * D / 8 / NT;  // 16-byte chunks per thread per tile (K and V each)
-  constexpr int TPR = (D / 8) / CPT;    // threads per key row
-  static_assert(CPT * NT == BN * D / 8 && NT / TPR == BN, "tile mapping");
+  constexpr int LPR = D / 8;            // threads per key row: consecutive lanes read consecutive 16-byte chunks
+  constexpr int RPI = NT / LPR;         // key rows per load instruction of the workgroup
+  constexpr int CPT = BN / RPI;         // 16-byte chunks per thread per tile (K and V each)
+  static_assert(CPT * RPI == BN && RPI * LPR == NT, "tile mapping");
 
   __shared__ __attribute__((aligned(16))) S Ks[BN][KP];
   __shared__ __attribute__((aligned(16))) S Vs[BN][KP];
@@ -113,26 +114,26 @@ attn_splitkv_kernel(SplitParams sp) {
   const int hi_max = wave_imax(row_ok && !empty ? k_hi : INT_MIN);
 
   const int n_t = k1 > k0 ? (k1 - k0 + BN - 1) / BN : 0;
-  const int row0 = tid / TPR, c0 = (tid % TPR) * CPT;
+  // Load i of a tile: thread tid reads 16-byte chunk tid % LPR of tile row i * RPI + tid / LPR, so one wave
+  // instruction covers 64 / LPR whole rows.
+  const int row0 = tid / LPR, c0 = tid % LPR;
   const S* kp = static_cast<const S*>(p.k) + b * p.k_sb + (int64_t)hk * p.k_sh + c0 * 8;
   const S* vp = static_cast<const S*>(p.v) + b * p.v_sb + (int64_t)hk * p.v_sh + c0 * 8;
   V8 kreg[CPT], vreg[CPT];
   // Rows past the split's end re-read its last key (masked below, finite: contributes exactly 0).
   auto load = [&](int t) {
-    const int key = min(k0 + t * BN + row0, k1 - 1);
-    const S* kt = kp + (int64_t)key * p.k_ss;
-    const S* vt = vp + (int64_t)key * p.v_ss;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      kreg[i] = ld16<V8>(kt + 8 * i);
-      vreg[i] = ld16<V8>(vt + 8 * i);
+      const int key = min(k0 + t * BN + i * RPI + row0, k1 - 1);
+      kreg[i] = ld16<V8>(kp + (int64_t)key * p.k_ss);
+      vreg[i] = ld16<V8>(vp + (int64_t)key * p.v_ss);
     }
   };
   auto store = [&]() {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      *reinterpret_cast<V8*>(&Ks[row0][(c0 + i) * 8]) = kreg[i];
-      *reinterpret_cast<V8*>(&Vs[row0][(c0 + i) * 8]) = vreg[i];
+      *reinterpret_cast<V8*>(&Ks[i * RPI + row0][c0 * 8]) = kreg[i];
+      *reinterpret_cast<V8*>(&Vs[i * RPI + row0][c0 * 8]) = vreg[i];
     }
   };
 
@@ -232,36 +233,64 @@ attn_splitkv_kernel(SplitParams sp) {
 
 // Merge of the splits of one row: o = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s, lse = M + log2 L (base 2, or
 // times ln 2). A row that sees no key at all gets L = 0, so o = NaN (the reference's softmax of an all -inf row)
-// and lse = -inf.
+// and lse = -inf. 256 threads per row: the weights go to LDS, then each thread sums 4 head-dim columns over every
+// (256 / (D/4))-th split (16-byte loads, four splits in flight) and the groups are added through LDS.
+constexpr int kMergeThreads = 256;
 template <typename T, int D>
-__global__ void __launch_bounds__(64) attn_splitkv_merge_kernel(SplitParams sp) {
+__global__ void __launch_bounds__(kMergeThreads) attn_splitkv_merge_kernel(SplitParams sp) {
   typedef typename T::scalar S;
   const AttnParams& p = sp.a;
   constexpr int kMaxSplits = 1024;
+  constexpr int CPR = D / 4;                    // float4 columns per row
+  constexpr int NG = kMergeThreads / CPR;       // split groups
   __shared__ float wts[kMaxSplits];
+  __shared__ f32x4 part[NG][CPR];
+  __shared__ float red[kMergeThreads / 64][2];
   const int row = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, wv = tid >> 6;
   const int64_t base = (((int64_t)b * p.Hkv + hk) * sp.M + row) * sp.splits;
+  const float* ml = sp.part_ml + base * 2;
   float M = -INFINITY;
-  for (int s = tid; s < sp.splits; s += 64) M = fmaxf(M, sp.part_ml[(base + s) * 2]);
+  for (int s = tid; s < sp.splits; s += kMergeThreads) M = fmaxf(M, ml[2 * s]);
   M = wave_max(M);
+  if ((tid & 63) == 0) red[wv][0] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(red[0][0], red[1][0]), fmaxf(red[2][0], red[3][0]));
   const float Mu = M == -INFINITY ? 0.f : M;
   float L = 0.f;
-  for (int s = tid; s < sp.splits; s += 64) {
-    const float wgt = fast_exp2(sp.part_ml[(base + s) * 2] - Mu);
+  for (int s = tid; s < sp.splits; s += kMergeThreads) {
+    const float wgt = fast_exp2(ml[2 * s] - Mu);
     wts[s] = wgt;
-    L += wgt * sp.part_ml[(base + s) * 2 + 1];
+    L += wgt * ml[2 * s + 1];
   }
   L = wave_sum(L);
+  if ((tid & 63) == 0) red[wv][1] = L;
+  __syncthreads();
+  L = (red[0][1] + red[1][1]) + (red[2][1] + red[3][1]);
+  const int col = tid % CPR, grp = tid / CPR;
+  const float* po = sp.part_o + base * D + 4 * col;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  int s = grp;
+  for (; s + 3 * NG < sp.splits; s += 4 * NG) {
+    const f32x4 a0 = *reinterpret_cast<const f32x4*>(po + (int64_t)s * D);
+    const f32x4 a1 = *reinterpret_cast<const f32x4*>(po + (int64_t)(s + NG) * D);
+    const f32x4 a2 = *reinterpret_cast<const f32x4*>(po + (int64_t)(s + 2 * NG) * D);
+    const f32x4 a3 = *reinterpret_cast<const f32x4*>(po + (int64_t)(s + 3 * NG) * D);
+    acc += wts[s] * a0 + wts[s + NG] * a1 + wts[s + 2 * NG] * a2 + wts[s + 3 * NG] * a3;
+  }
+  for (; s < sp.splits; s += NG) acc += wts[s] * *reinterpret_cast<const f32x4*>(po + (int64_t)s * D);
+  part[grp][col] = acc;
   __syncthreads();
   const int qh = row / p.Sq, qi = row - qh * p.Sq;
   const int h = hk * p.group + qh;
-  S* op = static_cast<S*>(p.o) + b * p.o_sb + (int64_t)qi * p.o_ss + (int64_t)h * p.o_sh;
-  const float inv = 1.0f / L;
-  for (int d = tid; d < D; d += 64) {
-    float od = 0.f;
-    for (int s = 0; s < sp.splits; ++s) od = fmaf(wts[s], sp.part_o[(base + s) * D + d], od);
-    op[d] = to_s<S>(od * inv);
+  if (tid < CPR) {
+    f32x4 o = part[0][tid];
+#pragma unroll
+    for (int gi = 1; gi < NG; ++gi) o += part[gi][tid];
+    const float inv = 1.0f / L;
+    S* op = static_cast<S*>(p.o) + b * p.o_sb + (int64_t)qi * p.o_ss + (int64_t)h * p.o_sh + 4 * tid;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) op[e] = to_s<S>(o[e] * inv);
   }
   if (tid == 0 && p.lse != nullptr) {
     const float l2 = M == -INFINITY ? -INFINITY : M + fast_log2(L);
@@ -276,7 +305,8 @@ void launch_splitkv(const SplitParams& sp, hipStream_t st) {
     hipLaunchKernelGGL((attn_splitkv_kernel<T, D, NW, true>), grid, dim3(64 * NW), 0, st, sp);
   else
     hipLaunchKernelGGL((attn_splitkv_kernel<T, D, NW, false>), grid, dim3(64 * NW), 0, st, sp);
-  hipLaunchKernelGGL((attn_splitkv_merge_kernel<T, D>), dim3(sp.M, sp.a.Hkv, sp.a.B), dim3(64), 0, st, sp);
+  hipLaunchKernelGGL((attn_splitkv_merge_kernel<T, D>), dim3(sp.M, sp.a.Hkv, sp.a.B), dim3(kMergeThreads), 0, st,
+                     sp);
 }
 
 template <typename T, int D>

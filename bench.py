@@ -326,7 +326,7 @@ def bench_splitkv(args, dev):
     q = torch.randn(B, Hq, D, generator=g, device=dev).half()
     kc = torch.randn(B, Hkv, L, D, generator=g, device=dev).half()
     vc = torch.randn(B, Hkv, L, D, generator=g, device=dev).half()
-    splits = 64
+    splits = 8  # best of 8 .. 128 in a sweep on MI355X (6.13 vs 5.80 TB/s at 64)
     ws = torch.empty(A.decode_workspace_bytes(B, Hq, D, splits), dtype=torch.uint8, device=dev)
     out = torch.empty_like(q)
     ms, info = _variant(lambda: A.decode_attention(q, kc, vc, splits=splits, out=out, workspace=ws), 10)

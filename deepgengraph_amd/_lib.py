@@ -59,6 +59,9 @@ SIGNATURES = {
     "dgg_topk_indices": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp]),
     "dgg_topk_select": (_i32, [_vp, _i64, _i64, _i64, _i32, _vp, _vp]),
     "dgg_roco_select": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "dgg_select_workspace_bytes": (_i64, [_i64, _i64]),
+    "dgg_topk_select_ws": (_i32, [_vp, _i64, _i64, _i64, _i32, _vp, _vp, _i64, _vp]),
+    "dgg_roco_select_ws": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
     "dgg_nonzero_workspace_bytes": (_i64, [_i64]),
     "dgg_nonzero": (_i32, [_vp, _i32, _i64p, _vp, _i64, _vp, _vp, _i64, _vp]),
     "dgg_clock_probe": (_i32, [_vp, _i64, _vp]),

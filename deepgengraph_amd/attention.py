@@ -441,9 +441,18 @@ def topk_indices(scores: torch.Tensor, k: int, largest: bool = True) -> torch.Te
     n = scores.shape[-1]
     rows = scores.numel() // n if n else 0
     out = torch.empty(*scores.shape[:-1], k, dtype=torch.int64, device=scores.device)
-    _lib.call("dgg_topk_select", _lib.ptr(scores), rows, n, int(k), 1 if largest else 0, _lib.ptr(out),
-              _lib.stream_handle(dev))
+    ws = _select_workspace(rows, n, scores.device)
+    _lib.call("dgg_topk_select_ws", _lib.ptr(scores), rows, n, int(k), 1 if largest else 0, _lib.ptr(out),
+              _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.stream_handle(dev))
     return out
+
+
+def _select_workspace(rows: int, n: int, device) -> torch.Tensor | None:
+    """Scratch of the selections over rows of more than 65536 keys (several workgroups per row); None below."""
+    need = int(_lib.load().dgg_select_workspace_bytes(rows, n))
+    if need <= 0:
+        return None
+    return torch.empty(need, dtype=torch.uint8, device=device)
 
 
 def roco_select(score: torch.Tensor, sq_score: torch.Tensor, q_len: int, recent: int, budget: int) -> torch.Tensor:
@@ -460,8 +469,9 @@ def roco_select(score: torch.Tensor, sq_score: torch.Tensor, q_len: int, recent:
     n = score.shape[-1]
     rows = score.numel() // n if n else 0
     out = torch.empty(*score.shape[:-1], budget + recent, dtype=torch.int64, device=score.device)
-    _lib.call("dgg_roco_select", _lib.ptr(score), _lib.ptr(sq_score), rows, n, int(q_len), int(recent), int(budget),
-              _lib.ptr(out), _lib.stream_handle(dev))
+    ws = _select_workspace(rows, n, score.device)
+    _lib.call("dgg_roco_select_ws", _lib.ptr(score), _lib.ptr(sq_score), rows, n, int(q_len), int(recent),
+              int(budget), _lib.ptr(out), _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.stream_handle(dev))
     return out
 
 

@@ -12,6 +12,8 @@
 // torch.topk leaves the order among equal values unspecified; these kernels define it: equal values are taken
 // lowest index first, in either direction. NaN (either sign) ranks above +inf, as torch.topk and torch.sort rank
 // it, and -0.0 equals +0.0.
+#include <algorithm>
+
 #include "common.h"
 
 namespace {
@@ -219,6 +221,330 @@ __global__ void __launch_bounds__(kTopkThreads) roco_select_kernel(const float* 
   write_taken(pick, rec, seg0, out + (int64_t)blockIdx.x * (budget + recent), (uint32_t)(budget + recent), sh);
 }
 
+// ------------------------------------------------------------------------------------------------
+// Rows longer than 65536 keys: the same selections (same key order, same tie rule, same output order) over many
+// workgroups per row, in passes through a caller-provided workspace. A row is cut into chunks of kSelChunk keys, one
+// 256-thread workgroup per (chunk, row); wave w of a chunk owns its contiguous kSelWaveSpan keys, 64 at a time
+// (lane l on key 64i + l), so a 64-bit ballot is one aligned word of a bit mask.
+//   1. four histogram passes: pass p counts the candidates whose key matches the digits chosen so far into 256 bins
+//      of its byte (LDS, then one global atomic per bin and workgroup); every workgroup of the next pass re-derives
+//      the chosen digits from the finished histograms (a 256-bin suffix scan per pass);
+//   2. per chunk, the number of candidates whose key equals K*, the k-th largest key;
+//   3. the selection as a bit mask: every candidate above K*, and candidates equal to K* while their rank among the
+//      equal ones (counted over the earlier chunks, the earlier waves of the chunk and the earlier lanes) is below
+//      the number still to take, i.e. lowest index first; plus the mask's population per chunk;
+//   4. the indices of one or two masks in ascending order (an index in both written twice), each chunk at the sum of
+//      the populations before it.
+// RoCo chains three selections: `recent` (largest std), `other` (smallest std), `pick` (largest mean among the
+// candidates of `other`'s mask), then writes pick and recent.
+// ------------------------------------------------------------------------------------------------
+constexpr int kSelThreads = 256;
+constexpr int kSelWaveSpan = 4096;                          // keys per wave per chunk (64 per lane)
+constexpr int kSelChunk = kSelWaveSpan * (kSelThreads / 64);  // keys per workgroup
+constexpr int kSelMaxN = 1 << 26;
+constexpr int kSelNSel = 3;                                 // selections a workspace holds (RoCo's three)
+
+struct SelWs {
+  uint32_t* hist;   // [rows][kSelNSel][4][256]
+  uint32_t* eqcnt;  // [rows][kSelNSel][chunks]
+  uint32_t* mcnt;   // [rows][kSelNSel][chunks]
+  uint64_t* mask;   // [rows][kSelNSel][words]
+  int chunks, words;
+};
+
+__host__ __device__ inline int64_t sel_align(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+// Workspace layout for `rows` rows of n keys; returns the total byte count (ws may be null to size only).
+inline int64_t sel_layout(int64_t rows, int64_t n, void* base, SelWs* ws) {
+  const int64_t chunks = (n + kSelChunk - 1) / kSelChunk, words = (n + 63) / 64;
+  const int64_t hist_b = sel_align(rows * kSelNSel * 1024 * 4);
+  const int64_t cnt_b = sel_align(rows * kSelNSel * chunks * 4);
+  const int64_t mask_b = sel_align(rows * kSelNSel * words * 8);
+  if (ws != nullptr) {
+    char* c = static_cast<char*>(base);
+    ws->hist = reinterpret_cast<uint32_t*>(c);
+    ws->eqcnt = reinterpret_cast<uint32_t*>(c + hist_b);
+    ws->mcnt = reinterpret_cast<uint32_t*>(c + hist_b + cnt_b);
+    ws->mask = reinterpret_cast<uint64_t*>(c + hist_b + 2 * cnt_b);
+    ws->chunks = (int)chunks;
+    ws->words = (int)words;
+  }
+  return hist_b + 2 * cnt_b + mask_b;
+}
+
+// Key sources: element j of row `row` as an order key (larger = taken first).
+struct KeyScores {  // topk_kernel's key: the score, complemented for the smallest-first direction
+  const float* x;
+  int n, largest;
+  __device__ __forceinline__ uint32_t operator()(int64_t row, int j) const {
+    const uint32_t k = order_key(x[row * n + j]);
+    return largest ? k : ~k;
+  }
+};
+struct KeyStd {  // roco_select_kernel's std key (complemented: the smallest first)
+  const float* s1;
+  const float* s2;
+  int n;
+  float rcp;
+  int complement;
+  __device__ __forceinline__ uint32_t operator()(int64_t row, int j) const {
+    const uint32_t k = order_key(roco_std(s1[row * n + j], s2[row * n + j], rcp));
+    return complement ? ~k : k;
+  }
+};
+struct KeyMean {  // roco_select_kernel's third key: roco_score / q_len
+  const float* s1;
+  int n;
+  float rcp;
+  __device__ __forceinline__ uint32_t operator()(int64_t row, int j) const {
+    return order_key(roco_mean(s1[row * n + j], rcp));
+  }
+};
+
+struct SelShared {
+  uint32_t hist[256];
+  uint32_t wsum[kSelThreads / 64];
+  uint32_t digit, rem;
+};
+
+// Digits chosen by the finished histogram passes 0 .. np-1 of a selection of k: prefix / pmask of the key bits
+// fixed so far and the number of candidates still to take among those matching them. All 256 threads call it.
+__device__ void sel_state(const uint32_t* H, int np, uint32_t k, uint32_t& prefix, uint32_t& pmask, uint32_t& rem,
+                          SelShared& sh) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  prefix = 0;
+  pmask = 0;
+  rem = k;
+  for (int ps = 0; ps < np; ++ps) {
+    const uint32_t c = H[ps * 256 + 255 - tid];  // thread t takes bin 255 - t
+    uint32_t incl = c;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t t = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += t;
+    }
+    if (lane == 63) sh.wsum[wv] = incl;
+    __syncthreads();
+    uint32_t base = 0;
+    for (int w2 = 0; w2 < wv; ++w2) base += sh.wsum[w2];
+    const uint32_t hi = base + incl, lo = hi - c;
+    if (lo < rem && hi >= rem) {
+      sh.digit = 255u - (uint32_t)tid;
+      sh.rem = rem - lo;
+    }
+    __syncthreads();
+    const int shift = 24 - 8 * ps;
+    prefix |= sh.digit << shift;
+    pmask |= 255u << shift;
+    rem = sh.rem;
+    __syncthreads();
+  }
+}
+
+__device__ __forceinline__ bool sel_cand(const uint64_t* cmask, int j) {
+  return cmask == nullptr || ((cmask[j >> 6] >> (j & 63)) & 1);
+}
+
+__global__ void __launch_bounds__(256) sel_zero_kernel(uint32_t* p, int64_t count) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) p[i] = 0u;
+}
+
+// Pass `ps` of the histogram of selection `sel` (k of the candidates: every key, or the bits of selection cand_sel).
+template <class KeyF>
+__global__ void __launch_bounds__(kSelThreads) sel_hist_kernel(KeyF kf, int n, SelWs ws, int sel, int ps, uint32_t k,
+                                                                int cand_sel) {
+  __shared__ SelShared sh;
+  const int64_t row = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  uint32_t* H = ws.hist + (row * kSelNSel + sel) * 1024;
+  const uint64_t* cm = cand_sel < 0 ? nullptr : ws.mask + (row * kSelNSel + cand_sel) * ws.words;
+  uint32_t prefix, pmask, rem;
+  sel_state(H, ps, k, prefix, pmask, rem, sh);
+  sh.hist[tid] = 0u;
+  __syncthreads();
+  const int shift = 24 - 8 * ps;
+  const int j0 = blockIdx.x * kSelChunk + wv * kSelWaveSpan + lane;
+  for (int i = 0; i < kSelWaveSpan / 64; ++i) {
+    const int j = j0 + 64 * i;
+    const bool act = j < n && sel_cand(cm, j);
+    uint32_t d = 0;
+    bool m = false;
+    if (act) {
+      const uint32_t key = kf(row, j);
+      m = (key & pmask) == prefix;
+      d = (key >> shift) & 255u;
+    }
+    // lanes whose digit equals the first active lane's add as one (the leading byte is nearly constant per row)
+    const uint64_t active = __ballot(m);
+    if (active) {
+      const int leader = __ffsll((long long)active) - 1;
+      const uint32_t d0 = __shfl(d, leader, 64);
+      const uint64_t same = __ballot(m && d == d0);
+      if (lane == leader) atomicAdd(&sh.hist[d0], (uint32_t)__popcll(same));
+      else if (m && d != d0) atomicAdd(&sh.hist[d], 1u);
+    }
+  }
+  __syncthreads();
+  if (sh.hist[tid] != 0u) atomicAdd(&H[ps * 256 + tid], sh.hist[tid]);
+}
+
+// Candidates equal to K* per chunk.
+template <class KeyF>
+__global__ void __launch_bounds__(kSelThreads) sel_eqcount_kernel(KeyF kf, int n, SelWs ws, int sel, uint32_t k,
+                                                                   int cand_sel) {
+  __shared__ SelShared sh;
+  const int64_t row = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint64_t* cm = cand_sel < 0 ? nullptr : ws.mask + (row * kSelNSel + cand_sel) * ws.words;
+  uint32_t kstar, pmask, rem;
+  sel_state(ws.hist + (row * kSelNSel + sel) * 1024, 4, k, kstar, pmask, rem, sh);
+  uint32_t eq = 0;
+  const int j0 = blockIdx.x * kSelChunk + wv * kSelWaveSpan + lane;
+  for (int i = 0; i < kSelWaveSpan / 64; ++i) {
+    const int j = j0 + 64 * i;
+    if (j < n && sel_cand(cm, j)) eq += kf(row, j) == kstar;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) eq += __shfl_xor(eq, off, 64);
+  if (lane == 0) sh.wsum[wv] = eq;
+  __syncthreads();
+  if (tid == 0) ws.eqcnt[(row * kSelNSel + sel) * ws.chunks + blockIdx.x] = sh.wsum[0] + sh.wsum[1] + sh.wsum[2] + sh.wsum[3];
+}
+
+// Sum of cnt[0 .. m) over the workgroup (every thread gets it).
+__device__ __forceinline__ uint32_t sel_block_sum(const uint32_t* cnt, int m, SelShared& sh) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  uint32_t v = 0;
+  for (int c = tid; c < m; c += kSelThreads) v += cnt[c];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  __syncthreads();
+  if (lane == 0) sh.wsum[wv] = v;
+  __syncthreads();
+  const uint32_t s = sh.wsum[0] + sh.wsum[1] + sh.wsum[2] + sh.wsum[3];
+  __syncthreads();
+  return s;
+}
+
+// The selection's bit mask and its population per chunk. k == 0 selects nothing.
+template <class KeyF>
+__global__ void __launch_bounds__(kSelThreads) sel_mark_kernel(KeyF kf, int n, SelWs ws, int sel, uint32_t k,
+                                                                int cand_sel) {
+  __shared__ SelShared sh;
+  __shared__ uint32_t weq[kSelThreads / 64];
+  const int64_t row = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint64_t* cm = cand_sel < 0 ? nullptr : ws.mask + (row * kSelNSel + cand_sel) * ws.words;
+  uint64_t* out = ws.mask + (row * kSelNSel + sel) * ws.words;
+  uint32_t kstar = 0, pmask, rem = 0, eq_before = 0;
+  if (k > 0) {
+    sel_state(ws.hist + (row * kSelNSel + sel) * 1024, 4, k, kstar, pmask, rem, sh);
+    eq_before = sel_block_sum(ws.eqcnt + (row * kSelNSel + sel) * ws.chunks, blockIdx.x, sh);
+  }
+  // this lane's 64 keys: above K* / equal to K*, one bit per step
+  uint64_t gtb = 0, eqb = 0;
+  uint32_t weq_cnt = 0;
+  const int j0 = blockIdx.x * kSelChunk + wv * kSelWaveSpan + lane;
+  if (k > 0) {
+    for (int i = 0; i < kSelWaveSpan / 64; ++i) {
+      const int j = j0 + 64 * i;
+      if (j < n && sel_cand(cm, j)) {
+        const uint32_t key = kf(row, j);
+        gtb |= (uint64_t)(key > kstar) << i;
+        eqb |= (uint64_t)(key == kstar) << i;
+      }
+    }
+    weq_cnt = __popcll(eqb);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) weq_cnt += __shfl_xor(weq_cnt, off, 64);
+  }
+  if (lane == 0) weq[wv] = weq_cnt;
+  __syncthreads();
+  uint32_t rank = eq_before;
+  for (int w2 = 0; w2 < wv; ++w2) rank += weq[w2];
+  const uint64_t lt = (1ull << lane) - 1;
+  uint32_t taken = 0;
+  for (int i = 0; i < kSelWaveSpan / 64; ++i) {
+    const int jw = blockIdx.x * kSelChunk + wv * kSelWaveSpan + 64 * i;  // first key of this step
+    if (jw >= n) break;
+    const bool e = (eqb >> i) & 1;
+    const uint64_t em = __ballot(e);
+    const uint32_t my_rank = rank + (uint32_t)__popcll(em & lt);
+    const bool take = ((gtb >> i) & 1) || (e && my_rank < rem);
+    const uint64_t tm = __ballot(take);
+    rank += (uint32_t)__popcll(em);
+    taken += (uint32_t)__popcll(tm);
+    if (lane == 0) out[jw >> 6] = tm;
+  }
+  __syncthreads();
+  if (lane == 0) sh.wsum[wv] = taken;
+  __syncthreads();
+  if (tid == 0) ws.mcnt[(row * kSelNSel + sel) * ws.chunks + blockIdx.x] = sh.wsum[0] + sh.wsum[1] + sh.wsum[2] + sh.wsum[3];
+}
+
+// Indices of mask A (and B, -1 = none) in ascending order into out [rows, out_k]; an index in both appears twice.
+__global__ void __launch_bounds__(kSelThreads) sel_emit_kernel(int n, SelWs ws, int sel_a, int sel_b,
+                                                                int64_t* __restrict__ out, int out_k) {
+  __shared__ SelShared sh;
+  __shared__ uint32_t wtot[kSelThreads / 64];
+  const int64_t row = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint64_t* ma = ws.mask + (row * kSelNSel + sel_a) * ws.words;
+  const uint64_t* mb = sel_b < 0 ? nullptr : ws.mask + (row * kSelNSel + sel_b) * ws.words;
+  uint32_t base = sel_block_sum(ws.mcnt + (row * kSelNSel + sel_a) * ws.chunks, blockIdx.x, sh);
+  if (sel_b >= 0) base += sel_block_sum(ws.mcnt + (row * kSelNSel + sel_b) * ws.chunks, blockIdx.x, sh);
+  const int w0 = (blockIdx.x * kSelChunk + wv * kSelWaveSpan) >> 6;  // first mask word of this wave
+  const int wend = min(ws.words, w0 + kSelWaveSpan / 64);
+  uint32_t tot = 0;
+  for (int w = w0 + lane; w < wend; w += 64) tot += __popcll(ma[w]) + (mb ? __popcll(mb[w]) : 0);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) tot += __shfl_xor(tot, off, 64);
+  if (lane == 0) wtot[wv] = tot;
+  __syncthreads();
+  for (int w2 = 0; w2 < wv; ++w2) base += wtot[w2];
+  const uint64_t lt = (1ull << lane) - 1;
+  int64_t* o = out + row * out_k;
+  for (int w = w0; w < wend; ++w) {
+    const uint64_t a = ma[w], b = mb ? mb[w] : 0ull;
+    if ((a | b) == 0) continue;
+    const int ba = (int)((a >> lane) & 1), bb = (int)((b >> lane) & 1);
+    uint32_t pos = base + (uint32_t)(__popcll(a & lt) + __popcll(b & lt));
+    const int64_t j = (int64_t)w * 64 + lane;
+    for (int r = 0; r < ba + bb; ++r, ++pos)
+      if (pos < (uint32_t)out_k) o[pos] = j;
+    base += (uint32_t)(__popcll(a) + __popcll(b));
+  }
+}
+
+// One selection of k among the candidates (cand_sel's mask, or every key) into mask `sel`.
+template <class KeyF>
+void sel_run(const KeyF& kf, int rows, int n, const SelWs& ws, int sel, uint32_t k, int cand_sel, hipStream_t st) {
+  const dim3 grid(ws.chunks, rows), block(kSelThreads);
+  if (k > 0) {
+    for (int ps = 0; ps < 4; ++ps) hipLaunchKernelGGL(sel_hist_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, ps, k,
+                                                      cand_sel);
+    hipLaunchKernelGGL(sel_eqcount_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, cand_sel);
+  }
+  hipLaunchKernelGGL(sel_mark_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, cand_sel);
+}
+
+void sel_zero_hist(const SelWs& ws, int rows, hipStream_t st) {
+  const int64_t count = (int64_t)rows * kSelNSel * 1024;
+  const unsigned blocks = (unsigned)std::min<int64_t>(1024, (count + 255) / 256);
+  hipLaunchKernelGGL(sel_zero_kernel, dim3(blocks), dim3(256), 0, st, ws.hist, count);
+}
+
+int sel_check_ws(const char* op, int64_t rows, int64_t n, void* workspace, int64_t workspace_bytes, SelWs* ws) {
+  DGG_REQUIRE(rows < 65536, DGG_ERR_SHAPE, "%s: more than 65535 rows of over 65536 keys (got %lld rows)", op,
+              (long long)rows);
+  const int64_t need = sel_layout(rows, n, workspace, ws);
+  DGG_REQUIRE(workspace != nullptr, DGG_ERR_NULL, "%s: rows of more than 65536 keys need a workspace", op);
+  DGG_REQUIRE(workspace_bytes >= need, DGG_ERR_WORKSPACE, "%s: workspace of %lld bytes < required %lld", op,
+              (long long)workspace_bytes, (long long)need);
+  DGG_REQUIRE(((uintptr_t)workspace & 255u) == 0, DGG_ERR_ALIGN, "%s: workspace must be 256-byte aligned", op);
+  return DGG_OK;
+}
+
 }  // namespace
 
 extern "C" int dgg_topk_select(const float* scores, int64_t rows, int64_t n, int64_t k, int largest,
@@ -269,5 +595,59 @@ extern "C" int dgg_roco_select(const float* score, const float* sq_score, int64_
     hipLaunchKernelGGL(roco_select_kernel<16>, grid, block, 0, st, score, sq_score, (int)n, rcp, r, b, out_idx);
   else
     hipLaunchKernelGGL(roco_select_kernel<64>, grid, block, 0, st, score, sq_score, (int)n, rcp, r, b, out_idx);
+  return dgg::check_launch("roco_select");
+}
+
+extern "C" int64_t dgg_select_workspace_bytes(int64_t rows, int64_t n) {
+  if (rows < 0 || n < 0) return -1;
+  if (n <= 65536) return 0;
+  return sel_layout(rows, n, nullptr, nullptr);
+}
+
+extern "C" int dgg_topk_select_ws(const float* scores, int64_t rows, int64_t n, int64_t k, int largest,
+                                  int64_t* out_idx, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (n <= 65536) return dgg_topk_select(scores, rows, n, k, largest, out_idx, stream);
+  DGG_REQUIRE(n <= kSelMaxN, DGG_ERR_SHAPE, "topk_indices: n must be <= 2^26 (got %lld)", (long long)n);
+  DGG_REQUIRE(rows >= 0, DGG_ERR_SHAPE, "topk_indices: bad row count %lld", (long long)rows);
+  DGG_REQUIRE(k >= 1 && k <= n, DGG_ERR_SHAPE, "topk_indices: k must be in [1, n] (got k=%lld, n=%lld)",
+              (long long)k, (long long)n);
+  if (rows == 0) return DGG_OK;
+  DGG_REQUIRE(scores && out_idx, DGG_ERR_NULL, "topk_indices: null pointer");
+  SelWs ws;
+  if (int rc = sel_check_ws("topk_indices", rows, n, workspace, workspace_bytes, &ws)) return rc;
+  hipStream_t st = dgg::as_stream(stream);
+  sel_zero_hist(ws, (int)rows, st);
+  sel_run(KeyScores{scores, (int)n, largest ? 1 : 0}, (int)rows, (int)n, ws, 0, (uint32_t)k, -1, st);
+  hipLaunchKernelGGL(sel_emit_kernel, dim3(ws.chunks, (unsigned)rows), dim3(kSelThreads), 0, st, (int)n, ws, 0, -1,
+                     out_idx, (int)k);
+  return dgg::check_launch("topk_indices");
+}
+
+extern "C" int dgg_roco_select_ws(const float* score, const float* sq_score, int64_t rows, int64_t n, int64_t q_len,
+                                  int64_t recent, int64_t budget, int64_t* out_idx, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  if (n <= 65536) return dgg_roco_select(score, sq_score, rows, n, q_len, recent, budget, out_idx, stream);
+  DGG_REQUIRE(n <= kSelMaxN, DGG_ERR_SHAPE, "roco_select: n must be <= 2^26 (got %lld)", (long long)n);
+  DGG_REQUIRE(rows >= 0, DGG_ERR_SHAPE, "roco_select: bad row count %lld", (long long)rows);
+  DGG_REQUIRE(q_len >= 1 && q_len <= (1ll << 24), DGG_ERR_SHAPE, "roco_select: q_len must be in [1, 2^24] (got %lld)",
+              (long long)q_len);
+  DGG_REQUIRE(recent >= 0 && recent <= n, DGG_ERR_SHAPE, "roco_select: recent must be in [0, n] (got %lld, n=%lld)",
+              (long long)recent, (long long)n);
+  DGG_REQUIRE(budget >= 0 && budget <= n - recent, DGG_ERR_SHAPE,
+              "roco_select: budget must be in [0, n - recent] (got %lld, n=%lld, recent=%lld)", (long long)budget,
+              (long long)n, (long long)recent);
+  if (rows == 0 || budget + recent == 0) return DGG_OK;
+  DGG_REQUIRE(score && sq_score && out_idx, DGG_ERR_NULL, "roco_select: null pointer");
+  SelWs ws;
+  if (int rc = sel_check_ws("roco_select", rows, n, workspace, workspace_bytes, &ws)) return rc;
+  hipStream_t st = dgg::as_stream(stream);
+  const float rcp = 1.0f / (float)q_len;  // torch's reciprocal of the Python divisor, in fp32
+  const int R = (int)rows, N = (int)n;
+  sel_zero_hist(ws, R, st);
+  sel_run(KeyStd{score, sq_score, N, rcp, 0}, R, N, ws, 0, (uint32_t)recent, -1, st);      // roco.py:56
+  sel_run(KeyStd{score, sq_score, N, rcp, 1}, R, N, ws, 1, (uint32_t)(n - recent), -1, st);  // roco.py:55
+  sel_run(KeyMean{score, N, rcp}, R, N, ws, 2, (uint32_t)budget, 1, st);                   // roco.py:57-58
+  hipLaunchKernelGGL(sel_emit_kernel, dim3(ws.chunks, (unsigned)rows), dim3(kSelThreads), 0, st, N, ws, 2, 0, out_idx,
+                     (int)(budget + recent));
   return dgg::check_launch("roco_select");
 }

@@ -216,6 +216,19 @@ int dgg_topk_select(const float* scores, int64_t rows, int64_t n, int64_t k, int
 int dgg_roco_select(const float* score, const float* sq_score, int64_t rows, int64_t n, int64_t q_len, int64_t recent,
                     int64_t budget, int64_t* out_idx, void* stream);
 
+/* Rows of more than 65536 keys (up to 2^26): dgg_topk_select and dgg_roco_select with the same results, computed
+ * by many workgroups per row in passes through a caller-provided workspace of
+ * dgg_select_workspace_bytes(rows, n) bytes (0 for n <= 65536, where these calls are dgg_topk_select /
+ * dgg_roco_select and ignore the workspace), 256-byte aligned; rows <= 65535 when n > 65536. No counterpart in the
+ * reference beyond the torch.topk calls they replace (models/h2o.py:51, models/snapkv.py:51, models/kf.py:54,
+ * models/roco.py:54-61), which have no size limit. */
+int64_t dgg_select_workspace_bytes(int64_t rows, int64_t n);
+int dgg_topk_select_ws(const float* scores, int64_t rows, int64_t n, int64_t k, int largest, int64_t* out_idx,
+                       void* workspace, int64_t workspace_bytes, void* stream);
+int dgg_roco_select_ws(const float* score, const float* sq_score, int64_t rows, int64_t n, int64_t q_len,
+                       int64_t recent, int64_t budget, int64_t* out_idx, void* workspace, int64_t workspace_bytes,
+                       void* stream);
+
 /* Decode attention (Attn.forward with q_len == 1, attn.py:22-23: no mask) as split-KV + LSE merge.
  * q [B, Hq, D] strides {b,h}; k/v cache [B, Hkv, L, D] strides {b,h,l}; o [B, Hq, D] strides {b,h}.
  * strides: 10 int64 = q{b,h}, k{b,h,l}, v{b,h,l}, o{b,h}.

@@ -178,6 +178,26 @@ def test_roco_select_validation(lib):
     assert lib.dgg_roco_select(None, None, 4, 100, 100, 0, 0, None, None) == OK    # nothing to select
 
 
+def test_select_workspace_validation(lib):
+    # rows of more than 65536 keys: sizes, the workspace and its alignment are checked before any launch; shorter rows
+    # go to the one-workgroup kernels and need no workspace
+    assert lib.dgg_select_workspace_bytes(4, 65536) == 0
+    need = lib.dgg_select_workspace_bytes(4, 1 << 20)
+    assert need > 4 * (1 << 20) // 8 * 3
+    assert lib.dgg_select_workspace_bytes(-1, 10) == -1
+    ws = ctypes.c_void_p(0x100000)
+    assert lib.dgg_topk_select_ws(FAKE, 4, 1 << 20, 10, 1, FAKE, ws, need - 1, None) == E_WS
+    assert lib.dgg_topk_select_ws(FAKE, 4, 1 << 20, 10, 1, FAKE, None, need, None) == E_NULL
+    assert lib.dgg_topk_select_ws(FAKE, 4, 1 << 20, 10, 1, FAKE, ctypes.c_void_p(0x100010), need, None) == E_ALIGN
+    assert lib.dgg_topk_select_ws(FAKE, 4, (1 << 26) + 1, 10, 1, FAKE, ws, 1 << 40, None) == E_SHAPE
+    assert lib.dgg_topk_select_ws(FAKE, 70000, 1 << 20, 10, 1, FAKE, ws, 1 << 40, None) == E_SHAPE
+    assert lib.dgg_topk_select_ws(FAKE, 4, 1 << 20, 0, 1, FAKE, ws, need, None) == E_SHAPE
+    assert lib.dgg_topk_select_ws(FAKE, 4, 100, 101, 1, FAKE, None, 0, None) == E_SHAPE  # short rows: as topk_select
+    assert lib.dgg_roco_select_ws(FAKE, FAKE, 4, 1 << 20, 10, 30, (1 << 20) - 29, FAKE, ws, need, None) == E_SHAPE
+    assert lib.dgg_roco_select_ws(FAKE, FAKE, 4, 1 << 20, 10, 30, 70, FAKE, ws, need - 1, None) == E_WS
+    assert lib.dgg_roco_select_ws(None, None, 4, 1 << 20, 10, 0, 0, None, None, 0, None) == OK  # nothing to select
+
+
 def test_decode_noalloc_validation(lib):
     # every argument is checked before the device's scratch is looked up (no GPU needed for these)
     s = _strides([32 * 128, 128, 32 * 4096 * 128, 4096 * 128, 128] + [32 * 4096 * 128, 4096 * 128, 128] + [32 * 128, 128])

@@ -439,6 +439,40 @@ def test_topk_smallest_and_nan_order(gpu):
             np.testing.assert_array_equal(got, osel.topk_indices(vals, k, largest), err_msg=f"n={n} k={k} {largest}")
 
 
+@pytest.mark.parametrize("n", [65537, 131072, 1048576])
+def test_topk_rows_longer_than_65536(gpu, n):
+    # the multi-workgroup selection (several chunks per row, passes through a workspace): ties, signed zeros,
+    # infinities and NaN, both directions, k at the edges and at chunk-crossing sizes
+    rng = np.random.default_rng(n)
+    pool = np.array([0.0, -0.0, 1.0, -1.0, 2.5, -7.0, np.inf, -np.inf, np.nan, -np.nan], dtype=np.float32)
+    vals = rng.integers(0, 1 << 12, size=(5, n)).astype(np.float32) / 64.0 - 30.0
+    vals[1] = rng.choice(pool, size=n)
+    vals[2, ::3] = np.nan
+    vals[3] = rng.integers(0, 3, size=n).astype(np.float32)
+    vals[4] = 1.0  # one value: the tie rule alone decides
+    x = torch.from_numpy(vals).to(gpu)
+    for k in (1, 256, 20000, n - 1, n):
+        progress(f"topk n={n} k={k}")
+        for largest in (True, False):
+            got = A.topk_indices(x, k, largest=largest).cpu().numpy()
+            np.testing.assert_array_equal(got, osel.topk_indices(vals, k, largest), err_msg=f"n={n} k={k} {largest}")
+
+
+@pytest.mark.parametrize("n,q_len,recent,budget", [(131072, 4096, 256, 512), (1048576, 100, 4096, 30000),
+                                                   (70000, 3, 0, 69999), (70000, 3, 70000, 0)])
+def test_roco_select_rows_longer_than_65536(gpu, n, q_len, recent, budget):
+    # RoCo's three chained selections over several workgroups per row, with ties and NaN std (negative variance)
+    rng = np.random.default_rng(n + recent)
+    s1 = rng.integers(0, 50, size=(2, n)).astype(np.float32)
+    s2 = rng.integers(0, 80, size=(2, n)).astype(np.float32) / 2.0
+    s1[1] = rng.random(n).astype(np.float32)
+    s2[1] = s1[1] * s1[1] / q_len + rng.random(n).astype(np.float32) * 1e-3
+    progress(f"roco_select n={n} recent={recent} budget={budget}")
+    got = A.roco_select(torch.from_numpy(s1).to(gpu), torch.from_numpy(s2).to(gpu), q_len, recent, budget)
+    np.testing.assert_array_equal(got.cpu().numpy(), osel.roco_select(s1, s2, q_len, recent, budget),
+                                  err_msg=f"n={n} q_len={q_len} recent={recent} budget={budget}")
+
+
 def _roco_torch_gpu(s1, s2, q_len, recent, budget):
     """models/roco.py:54-61 as the reference writes it, run by torch on the GPU (its rounding of / q_len)."""
     std = torch.sqrt(s2 / q_len - (s1 / q_len) ** 2)

@@ -211,8 +211,12 @@ def bench_prestep(args, dev):
     nb = e * (2 * pre["x"].numel() + pre["w_norm"].numel())
     res["rms_norm_64x4096_f16"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1))
     ms = _events_time(lambda: ops.silu_and_mul(act, pre["gate_up"]), 20, 3)
-    nb = e * (pre["gate_up"].numel() + act.numel())
-    res["silu_and_mul_64x11008_f16"] = dict(us=round(ms * 1e3, 2), gbps=round(nb / (ms * 1e-3) / 1e9, 1))
+    nb2 = e * (pre["gate_up"].numel() + act.numel())
+    res["silu_and_mul_64x11008_f16"] = dict(us=round(ms * 1e3, 2), gbps=round(nb2 / (ms * 1e-3) / 1e9, 1))
+    # the pre-step as it runs (llama.decode_prestep): both ops in one launch
+    ms = _events_time(lambda: ops.rms_norm_silu_and_mul(normed, pre["x"], pre["w_norm"], C.LLAMA_EPS, act,
+                                                        pre["gate_up"]), 20, 3)
+    res["prestep_one_launch_f16"] = dict(us=round(ms * 1e3, 2), gbps=round((nb + nb2) / (ms * 1e-3) / 1e9, 1))
     # config-2 sized elementwise kernels (bandwidth-meaningful sizes)
     x = torch.randn(4096, 4096, device=dev).bfloat16()
     w = torch.ones(4096, device=dev).bfloat16()

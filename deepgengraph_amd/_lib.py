@@ -40,6 +40,8 @@ SIGNATURES = {
     "dgg_rms_norm": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _f32, _vp]),
     "dgg_fused_add_rms_norm": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _f32, _vp]),
     "dgg_silu_and_mul": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp]),
+    "dgg_rms_norm_silu_and_mul": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp, _vp, _i64, _i64, _i64, _i64,
+                                         _i32, _vp]),
     "dgg_rotary_embedding_online": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _f32, _vp]),
     "dgg_attn_prefill": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64p, _f32, _f32,
                                 _i64, _u32, _i32, _vp]),

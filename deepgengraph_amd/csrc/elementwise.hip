@@ -2,6 +2,8 @@
 // SiLU-and-mul and online rotary embedding. All are HBM-bound: 16-byte vector loads/stores, one pass
 // over the data (the row of an RMSNorm is held in registers between the reduction and the scaling),
 // fp32 arithmetic, and rounding to the storage type at the points where the reference rounds.
+#include <algorithm>
+
 #include "common.h"
 
 namespace {
@@ -53,16 +55,13 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // output from the rounded residual.
 // ---------------------------------------------------------------------------------------------
 template <typename T, int NV, bool RESID>
-__global__ void __launch_bounds__(1024) rms_norm_vec_kernel(typename T::scalar* __restrict__ out,
-                                                             const typename T::scalar* __restrict__ in,
-                                                             typename T::scalar* __restrict__ res,
-                                                             const typename T::scalar* __restrict__ w,
-                                                             int hidden, int64_t in_rs, int64_t out_rs,
-                                                             int64_t res_rs, float eps) {
+__device__ __forceinline__ void rms_row_vec(int64_t row, typename T::scalar* __restrict__ out,
+                                            const typename T::scalar* __restrict__ in,
+                                            typename T::scalar* __restrict__ res,
+                                            const typename T::scalar* __restrict__ w, int hidden, int64_t in_rs,
+                                            int64_t out_rs, int64_t res_rs, float eps, float* red) {
   typedef typename VecOf<T>::type V;
   constexpr int EPV = VecOf<T>::EPV;
-  __shared__ float red[16];
-  const int64_t row = blockIdx.x;
   const int nvec = hidden / EPV;
   const typename T::scalar* x = in + row * in_rs;
   float vals[NV][EPV];
@@ -111,6 +110,17 @@ __global__ void __launch_bounds__(1024) rms_norm_vec_kernel(typename T::scalar* 
   }
 }
 
+template <typename T, int NV, bool RESID>
+__global__ void __launch_bounds__(1024) rms_norm_vec_kernel(typename T::scalar* __restrict__ out,
+                                                             const typename T::scalar* __restrict__ in,
+                                                             typename T::scalar* __restrict__ res,
+                                                             const typename T::scalar* __restrict__ w,
+                                                             int hidden, int64_t in_rs, int64_t out_rs,
+                                                             int64_t res_rs, float eps) {
+  __shared__ float red[16];
+  rms_row_vec<T, NV, RESID>(blockIdx.x, out, in, res, w, hidden, in_rs, out_rs, res_rs, eps, red);
+}
+
 // Scalar fallback for any hidden size / alignment: two passes over the row (second pass re-reads it).
 template <typename T, bool RESID>
 __global__ void __launch_bounds__(1024) rms_norm_scalar_kernel(typename T::scalar* __restrict__ out,
@@ -143,16 +153,16 @@ __global__ void __launch_bounds__(1024) rms_norm_scalar_kernel(typename T::scala
 // ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ float silu_f(float g) { return g * fast_rcp(1.f + fast_exp2(-g * kLog2e)); }
 
+// Vector SiLU-and-mul over the 16-byte chunks t = blk * blockDim + tid, stepping by nblk * blockDim.
 template <typename T>
-__global__ void __launch_bounds__(256) silu_and_mul_vec_kernel(typename T::scalar* __restrict__ out,
-                                                                const typename T::scalar* __restrict__ in,
-                                                                int64_t rows, int64_t d, int64_t in_rs,
-                                                                int64_t out_rs) {
+__device__ __forceinline__ void silu_vec_range(typename T::scalar* __restrict__ out,
+                                               const typename T::scalar* __restrict__ in, int64_t rows, int64_t d,
+                                               int64_t in_rs, int64_t out_rs, int64_t blk, int64_t nblk) {
   typedef typename VecOf<T>::type V;
   constexpr int EPV = VecOf<T>::EPV;
   const int64_t vpr = d / EPV;
   const int64_t total = rows * vpr;
-  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+  for (int64_t t = blk * blockDim.x + threadIdx.x; t < total; t += nblk * blockDim.x) {
     const int64_t r = t / vpr, c = (t - r * vpr) * EPV;
     const typename T::scalar* src = in + r * in_rs;
     V g = ld16<V>(src + c);
@@ -162,6 +172,37 @@ __global__ void __launch_bounds__(256) silu_and_mul_vec_kernel(typename T::scala
     for (int e = 0; e < EPV; ++e) o[e] = to_s<typename T::scalar>(round_t<T>(silu_f(to_f(g[e]))) * to_f(u[e]));
     st16<V>(out + r * out_rs + c, o);
   }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) silu_and_mul_vec_kernel(typename T::scalar* __restrict__ out,
+                                                                const typename T::scalar* __restrict__ in,
+                                                                int64_t rows, int64_t d, int64_t in_rs,
+                                                                int64_t out_rs) {
+  silu_vec_range<T>(out, in, rows, d, in_rs, out_rs, blockIdx.x, gridDim.x);
+}
+
+// ---------------------------------------------------------------------------------------------
+// RMSNorm and SiLU-and-mul in one launch (the decode pre-step: a few rows of each, where each op alone is a few
+// microseconds of launch ramp): workgroups 0 .. norm_rows-1 normalise one row each, the others split the SiLU
+// chunks between them.
+// ---------------------------------------------------------------------------------------------
+template <typename T, int NV>
+__global__ void __launch_bounds__(1024) rms_silu_kernel(typename T::scalar* __restrict__ norm_out,
+                                                         const typename T::scalar* __restrict__ norm_in,
+                                                         const typename T::scalar* __restrict__ w, int hidden,
+                                                         int64_t norm_in_rs, int64_t norm_out_rs, float eps,
+                                                         int norm_rows, typename T::scalar* __restrict__ act_out,
+                                                         const typename T::scalar* __restrict__ act_in,
+                                                         int64_t act_rows, int64_t d, int64_t act_in_rs,
+                                                         int64_t act_out_rs) {
+  __shared__ float red[16];
+  if ((int)blockIdx.x < norm_rows)
+    rms_row_vec<T, NV, false>(blockIdx.x, norm_out, norm_in, nullptr, w, hidden, norm_in_rs, norm_out_rs, 0, eps,
+                              red);
+  else
+    silu_vec_range<T>(act_out, act_in, act_rows, d, act_in_rs, act_out_rs, blockIdx.x - norm_rows,
+                      gridDim.x - norm_rows);
 }
 
 template <typename T>
@@ -325,6 +366,58 @@ int silu_dispatch(void* out, const void* in, int64_t rows, int64_t d, int64_t in
   return dgg::check_launch("silu_and_mul");
 }
 
+template <typename T, int NV>
+void launch_rms_silu(int threads, unsigned silu_blocks, void* norm_out, const void* norm_in, const void* w,
+                     int64_t norm_rows, int hidden, int64_t n_in_rs, int64_t n_out_rs, float eps, void* act_out,
+                     const void* act_in, int64_t act_rows, int64_t d, int64_t a_in_rs, int64_t a_out_rs,
+                     hipStream_t st) {
+  typedef typename T::scalar S;
+  hipLaunchKernelGGL((rms_silu_kernel<T, NV>), dim3((unsigned)norm_rows + silu_blocks), dim3(threads), 0, st,
+                     (S*)norm_out, (const S*)norm_in, (const S*)w, hidden, n_in_rs, n_out_rs, eps, (int)norm_rows,
+                     (S*)act_out, (const S*)act_in, act_rows, d, a_in_rs, a_out_rs);
+}
+
+// One launch when both ops take the vector path and the norm rows fit one workgroup each; otherwise the two
+// kernels one after the other.
+template <typename T>
+int rms_silu_dispatch(void* norm_out, const void* norm_in, const void* w, int64_t norm_rows, int64_t hidden,
+                      int64_t n_in_rs, int64_t n_out_rs, float eps, void* act_out, const void* act_in, int64_t act_rows,
+                      int64_t d, int64_t a_in_rs, int64_t a_out_rs, hipStream_t st) {
+  constexpr int EPV = VecOf<T>::EPV;
+  const bool vec = hidden % EPV == 0 && n_in_rs % EPV == 0 && n_out_rs % EPV == 0 && dgg::aligned16(norm_out) &&
+                   dgg::aligned16(norm_in) && dgg::aligned16(w) && d % EPV == 0 && a_in_rs % EPV == 0 &&
+                   a_out_rs % EPV == 0 && dgg::aligned16(act_out) && dgg::aligned16(act_in);
+  const int64_t nvec = hidden / EPV;
+  if (!vec || nvec > 8 * 1024 || norm_rows == 0 || act_rows == 0 || norm_rows > (1 << 20)) {
+    if (norm_rows > 0)
+      if (int rc = rms_dispatch<T, false>(norm_out, norm_in, nullptr, w, norm_rows, hidden, n_in_rs, n_out_rs, 0, eps,
+                                          st))
+        return rc;
+    if (act_rows > 0) return silu_dispatch<T>(act_out, act_in, act_rows, d, a_in_rs, a_out_rs, st);
+    return DGG_OK;
+  }
+  // one 16-byte chunk of the norm row per thread (as the few-row RMSNorm launch), up to 8 for wide rows
+  int threads = (int)((nvec + 63) / 64 * 64);
+  if (threads > 1024) threads = 1024;
+  const int64_t nv = (nvec + threads - 1) / threads;
+  const int64_t silu_vecs = act_rows * (d / EPV);
+  const unsigned silu_blocks = (unsigned)std::min<int64_t>(256 * 64, (silu_vecs + threads - 1) / threads);
+  const int h = (int)hidden;
+  if (nv <= 1)
+    launch_rms_silu<T, 1>(threads, silu_blocks, norm_out, norm_in, w, norm_rows, h, n_in_rs, n_out_rs, eps, act_out,
+                          act_in, act_rows, d, a_in_rs, a_out_rs, st);
+  else if (nv <= 2)
+    launch_rms_silu<T, 2>(threads, silu_blocks, norm_out, norm_in, w, norm_rows, h, n_in_rs, n_out_rs, eps, act_out,
+                          act_in, act_rows, d, a_in_rs, a_out_rs, st);
+  else if (nv <= 4)
+    launch_rms_silu<T, 4>(threads, silu_blocks, norm_out, norm_in, w, norm_rows, h, n_in_rs, n_out_rs, eps, act_out,
+                          act_in, act_rows, d, a_in_rs, a_out_rs, st);
+  else
+    launch_rms_silu<T, 8>(threads, silu_blocks, norm_out, norm_in, w, norm_rows, h, n_in_rs, n_out_rs, eps, act_out,
+                          act_in, act_rows, d, a_in_rs, a_out_rs, st);
+  return dgg::check_launch("rms_norm_silu_and_mul");
+}
+
 template <typename T>
 int rotary_dispatch(const int32_t* pos, void* q, void* k, int64_t tokens, int64_t hq, int64_t hk, int64_t D,
                     int64_t q_rs, int64_t k_rs, float theta, hipStream_t st) {
@@ -401,6 +494,35 @@ extern "C" int dgg_silu_and_mul(void* out, const void* input, int64_t rows, int6
     case DGG_F16: return silu_dispatch<F16>(out, input, rows, d, in_row_stride, out_row_stride, st);
     case DGG_BF16: return silu_dispatch<BF16>(out, input, rows, d, in_row_stride, out_row_stride, st);
     default: return silu_dispatch<F32>(out, input, rows, d, in_row_stride, out_row_stride, st);
+  }
+}
+
+extern "C" int dgg_rms_norm_silu_and_mul(void* norm_out, const void* norm_in, const void* weight, int64_t norm_rows,
+                                         int64_t hidden, int64_t norm_in_row_stride, int64_t norm_out_row_stride,
+                                         float epsilon, void* act_out, const void* act_in, int64_t act_rows, int64_t d,
+                                         int64_t act_in_row_stride, int64_t act_out_row_stride, int dtype,
+                                         void* stream) {
+  DGG_REQUIRE(dgg::valid_dtype(dtype), DGG_ERR_DTYPE, "rms_norm_silu_and_mul: unsupported dtype code %d", dtype);
+  if (int rc = check_rows("rms_norm_silu_and_mul", norm_rows, hidden, norm_in_row_stride, norm_out_row_stride, hidden))
+    return rc;
+  if (int rc = check_rows("rms_norm_silu_and_mul", act_rows, d, act_in_row_stride, act_out_row_stride, 2 * d)) return rc;
+  if (norm_rows == 0 && act_rows == 0) return DGG_OK;
+  DGG_REQUIRE((norm_rows == 0 || (norm_out && norm_in && weight)) && (act_rows == 0 || (act_out && act_in)),
+              DGG_ERR_NULL, "rms_norm_silu_and_mul: null pointer");
+  hipStream_t st = dgg::as_stream(stream);
+  switch (dtype) {
+    case DGG_F16:
+      return rms_silu_dispatch<F16>(norm_out, norm_in, weight, norm_rows, hidden, norm_in_row_stride,
+                                    norm_out_row_stride, epsilon, act_out, act_in, act_rows, d, act_in_row_stride,
+                                    act_out_row_stride, st);
+    case DGG_BF16:
+      return rms_silu_dispatch<BF16>(norm_out, norm_in, weight, norm_rows, hidden, norm_in_row_stride,
+                                     norm_out_row_stride, epsilon, act_out, act_in, act_rows, d, act_in_row_stride,
+                                     act_out_row_stride, st);
+    default:
+      return rms_silu_dispatch<F32>(norm_out, norm_in, weight, norm_rows, hidden, norm_in_row_stride,
+                                    norm_out_row_stride, epsilon, act_out, act_in, act_rows, d, act_in_row_stride,
+                                    act_out_row_stride, st);
   }
 }
 

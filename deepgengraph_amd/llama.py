@@ -64,10 +64,9 @@ class LlamaAttentionBlock:
 
 def decode_prestep(x: torch.Tensor, w_norm: torch.Tensor, gate_up: torch.Tensor, eps: float = 1e-6):
     """Config 5 pre-step: RMSNorm of the query-side hidden state and SiLU-and-mul of the MLP activation pair
-    (LlamaLayer's RmsNorm.forward and MLP.forward elementwise parts, llama_base.py:287-289, 305-314).
-    Returns (normed, act)."""
+    (LlamaLayer's RmsNorm.forward and MLP.forward elementwise parts, llama_base.py:287-289, 305-314), both in one
+    launch. Returns (normed, act)."""
     normed = torch.empty_like(x)
-    ops.rms_norm(normed, x, w_norm, eps)
     act = torch.empty(*gate_up.shape[:-1], gate_up.shape[-1] // 2, dtype=gate_up.dtype, device=gate_up.device)
-    ops.silu_and_mul(act, gate_up)
+    ops.rms_norm_silu_and_mul(normed, x, w_norm, eps, act, gate_up)
     return normed, act

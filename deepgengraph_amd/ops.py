@@ -78,6 +78,34 @@ def silu_and_mul(out: torch.Tensor, input: torch.Tensor) -> None:
               _lib.dtype_code(input.dtype), _lib.stream_handle(dev))
 
 
+def rms_norm_silu_and_mul(norm_out: torch.Tensor, norm_input: torch.Tensor, weight: torch.Tensor, epsilon: float,
+                          act_out: torch.Tensor, act_input: torch.Tensor) -> None:
+    """rms_norm(norm_out, norm_input, weight, epsilon) and silu_and_mul(act_out, act_input) in one launch (the decode
+    step's RmsNorm.forward and MLP.forward elementwise parts, llama_base.py:287-289, 305-314). Same checks and results
+    as the two ops; no counterpart as one op in the reference's _csrc."""
+    dev = _lib.require_gpu(norm_out, norm_input, weight, act_out, act_input)
+    dt = norm_input.dtype
+    if not (norm_out.dtype == dt == weight.dtype == act_out.dtype == act_input.dtype):
+        raise RuntimeError("rms_norm_silu_and_mul: all tensors must share one dtype")
+    hidden = norm_input.shape[-1]
+    if norm_out.shape != norm_input.shape:
+        raise RuntimeError("rms_norm_silu_and_mul: norm_out shape differs from norm_input")
+    if weight.numel() != hidden or (weight.dim() > 0 and weight.stride(-1) != 1 and hidden > 1):
+        raise RuntimeError(f"rms_norm_silu_and_mul: weight must be a contiguous vector of {hidden} elements")
+    if act_input.shape[-1] % 2:
+        raise RuntimeError(f"rms_norm_silu_and_mul: act_input last dimension {act_input.shape[-1]} must be even")
+    d = act_input.shape[-1] // 2
+    if act_out.shape[:-1] != act_input.shape[:-1] or act_out.shape[-1] != d:
+        raise RuntimeError("rms_norm_silu_and_mul: act_out shape does not match act_input")
+    n_rows, n_in_rs = _rows(norm_input, "rms_norm_silu_and_mul norm_input")
+    _, n_out_rs = _rows(norm_out, "rms_norm_silu_and_mul norm_out")
+    a_rows, a_in_rs = _rows(act_input, "rms_norm_silu_and_mul act_input")
+    _, a_out_rs = _rows(act_out, "rms_norm_silu_and_mul act_out")
+    _lib.call("dgg_rms_norm_silu_and_mul", _lib.ptr(norm_out), _lib.ptr(norm_input), _lib.ptr(weight), n_rows, hidden,
+              n_in_rs, n_out_rs, float(epsilon), _lib.ptr(act_out), _lib.ptr(act_input), a_rows, d, a_in_rs, a_out_rs,
+              _lib.dtype_code(dt), _lib.stream_handle(dev))
+
+
 def rotary_embedding_online(positions: torch.Tensor, query: torch.Tensor, key: torch.Tensor | None, head_size: int,
                             rope_theta: float) -> None:
     """csrc/pos_encoding.cu:180-199: NeoX rotary of query [..., Hq*D] and key [..., Hk*D], in place.

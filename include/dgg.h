@@ -78,6 +78,15 @@ int dgg_fused_add_rms_norm(void* input, void* residual, const void* weight, int6
 int dgg_silu_and_mul(void* out, const void* input, int64_t rows, int64_t d, int64_t in_row_stride,
                      int64_t out_row_stride, int dtype, void* stream);
 
+/* dgg_rms_norm on [norm_rows, hidden] and dgg_silu_and_mul on [act_rows, 2d] in one launch (no counterpart as one
+ * call in the reference: the two ops of the decode step's RmsNorm.forward and MLP.forward, llama_base.py:287-289,
+ * 305-314, each csrc/norm.cu:85-98 and csrc/activation.cu:24-34). Results are those of the two calls; the one-launch
+ * form needs 16-byte aligned rows (else the two kernels run one after the other). Either row count may be 0. */
+int dgg_rms_norm_silu_and_mul(void* norm_out, const void* norm_in, const void* weight, int64_t norm_rows,
+                              int64_t hidden, int64_t norm_in_row_stride, int64_t norm_out_row_stride, float epsilon,
+                              void* act_out, const void* act_in, int64_t act_rows, int64_t d,
+                              int64_t act_in_row_stride, int64_t act_out_row_stride, int dtype, void* stream);
+
 /* csrc/pos_encoding.cu:180-199 rotary_embedding_online(positions, query, key, head_size, rope_theta):
  * NeoX pairing (i, i + D/2), angle = pos / theta^(2i/D) in fp32, in place on query [tokens, head_num*D]
  * and key [tokens, kv_head_num*D] with row strides q_row_stride / k_row_stride.

@@ -106,6 +106,35 @@ def test_silu_and_mul(gpu, rows, d, dtype):
         assert exact > 0.99, f"only {exact:.4f} of elements bit-identical to the oracle"
 
 
+@pytest.mark.parametrize("nrows,hidden,arows,d,dtype", [
+    (64, 4096, 64, 11008, torch.float16),    # config 5 pre-step: one launch
+    (3, 65536, 7, 96, torch.bfloat16),       # widest norm row (8 chunks per thread)
+    (5, 1001, 4, 300, torch.float16),        # odd norm width: the two kernels one after the other
+    (2, 512, 3, 1001, torch.bfloat16),       # odd SiLU width: the same
+    (9, 1000, 6, 64, torch.float32),
+    (0, 4096, 5, 128, torch.bfloat16),       # nothing to normalise
+    (4, 4096, 0, 128, torch.bfloat16),       # nothing to activate
+])
+def test_rms_norm_silu_and_mul_one_launch(gpu, nrows, hidden, arows, d, dtype):
+    # the pre-step's two ops in one launch: bit-identical to the two separate ops, and within tolerance of the oracle
+    x = _randn((nrows, hidden), dtype, 21)
+    w = _randn((hidden,), dtype, 22, 0.02, 1.0)
+    gu = _randn((arows, 2 * d), dtype, 23, 3.0)
+    xg, wg, gug = x.to(gpu), w.to(gpu), gu.to(gpu)
+    normed, act = torch.empty_like(xg), torch.empty(arows, d, dtype=dtype, device=gpu)
+    ops.rms_norm_silu_and_mul(normed, xg, wg, 1e-6, act, gug)
+    n2, a2 = torch.empty_like(xg), torch.empty_like(act)
+    if nrows:
+        ops.rms_norm(n2, xg, wg, 1e-6)
+    if arows:
+        ops.silu_and_mul(a2, gug)
+    assert torch.equal(normed.cpu(), n2.cpu()) and torch.equal(act.cpu(), a2.cpu()), "differs from the two ops"
+    if nrows:
+        assert_close(normed.cpu().float(), oe.rms_norm(x, w, 1e-6).float(), *TOL[dtype], "rms_norm part")
+    if arows:
+        assert_close(act.cpu().float(), oe.silu_and_mul(gu).float(), *TOL[dtype], "silu_and_mul part")
+
+
 def test_silu_and_mul_golden(gpu):
     g = load_golden("silu_and_mul_f16")
     x = torch.from_numpy(g["x"]).half().to(gpu)

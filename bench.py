@@ -344,6 +344,28 @@ def bench_splitkv(args, dev):
     return res
 
 
+def bench_longsel(args, dev):
+    """H2O / SnapKV top-256 (models/h2o.py:51-52) and RoCo's selection (models/roco.py:54-61) over rows longer than
+    65536 keys (32 heads, long-context KV caches): the multi-workgroup radix select, against torch.topk + sort on the
+    same GPU."""
+    from deepgengraph_amd import attention as A
+
+    res = {}
+    for n in (131072, 1048576):
+        g = torch.Generator(device=dev).manual_seed(n)
+        cs = torch.rand(32, n, generator=g, device=dev)
+        ms, info = _variant(lambda: A.topk_indices(cs, 256), 10)
+        ms_t, _ = _variant(lambda: torch.topk(cs, k=256, dim=-1, sorted=True)[1].sort(dim=-1)[0], 10)
+        res[f"topk256_32x{n}"] = dict(us=round(ms * 1e3, 2), gbps=round(cs.numel() * 4 / (ms * 1e-3) / 1e9, 1),
+                                      torch_us=round(ms_t * 1e3, 2), **info)
+    n = 131072
+    s1 = torch.rand(32, n, device=dev) * 64
+    s2 = s1 * s1 / 4096 + torch.rand(32, n, device=dev)
+    ms, info = _variant(lambda: A.roco_select(s1, s2, 4096, 256, 512), 10)
+    res[f"roco_select_32x{n}"] = dict(us=round(ms * 1e3, 2), **info)
+    return res
+
+
 def bench_block(args, dev):
     from deepgengraph_amd import configs as C
     from deepgengraph_amd.llama import LlamaAttentionBlock
@@ -417,7 +439,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--sections", default="prefill,decode,splitkv,prestep,variants,block")
+    ap.add_argument("--sections", default="prefill,decode,splitkv,prestep,variants,longsel,block")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-steady", action="store_true", help="skip the steady-clock figure (short profiled runs)")
     args = ap.parse_args()
@@ -441,6 +463,8 @@ def main():
         extra["elementwise"] = bench_prestep(args, dev)
     if "variants" in sections:
         extra["variants"] = bench_variants(args, dev)
+    if "longsel" in sections:
+        extra["long_selection"] = bench_longsel(args, dev)
     if "block" in sections:
         blk = bench_block(args, dev)
         extra["cfg2_block_ms"] = blk["ms"]

@@ -239,7 +239,8 @@ __global__ void __launch_bounds__(kTopkThreads) roco_select_kernel(const float* 
 // candidates of `other`'s mask), then writes pick and recent.
 // ------------------------------------------------------------------------------------------------
 constexpr int kSelThreads = 256;
-constexpr int kSelWaveSpan = 4096;                          // keys per wave per chunk (64 per lane)
+constexpr int kSelPer = 16;                                 // keys per lane per chunk, loaded back to back
+constexpr int kSelWaveSpan = 64 * kSelPer;                  // keys per wave per chunk
 constexpr int kSelChunk = kSelWaveSpan * (kSelThreads / 64);  // keys per workgroup
 constexpr int kSelMaxN = 1 << 26;
 constexpr int kSelNSel = 3;                                 // selections a workspace holds (RoCo's three)
@@ -250,13 +251,19 @@ struct SelWs {
   uint32_t* mcnt;   // [rows][kSelNSel][chunks]
   uint64_t* mask;   // [rows][kSelNSel][words]
   int chunks, words;
+  int spc;          // kSelChunk-key sub-chunks per workgroup (a chunk is spc * kSelChunk keys)
 };
 
 __host__ __device__ inline int64_t sel_align(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
-// Workspace layout for `rows` rows of n keys; returns the total byte count (ws may be null to size only).
+// Workspace layout for `rows` rows of n keys; returns the total byte count (ws may be null to size only). A workgroup
+// takes enough sub-chunks that there are about 2048 workgroups in all: more would multiply the global histogram
+// atomics on the same 256 bins per row, fewer would leave the chip idle.
 inline int64_t sel_layout(int64_t rows, int64_t n, void* base, SelWs* ws) {
-  const int64_t chunks = (n + kSelChunk - 1) / kSelChunk, words = (n + 63) / 64;
+  const int64_t sub = (n + kSelChunk - 1) / kSelChunk;
+  const int64_t want = std::max<int64_t>(1, (2048 + rows - 1) / std::max<int64_t>(rows, 1));
+  const int64_t spc = std::max<int64_t>(1, (sub + want - 1) / want);
+  const int64_t chunks = (sub + spc - 1) / spc, words = (n + 63) / 64;
   const int64_t hist_b = sel_align(rows * kSelNSel * 1024 * 4);
   const int64_t cnt_b = sel_align(rows * kSelNSel * chunks * 4);
   const int64_t mask_b = sel_align(rows * kSelNSel * words * 8);
@@ -268,6 +275,7 @@ inline int64_t sel_layout(int64_t rows, int64_t n, void* base, SelWs* ws) {
     ws->mask = reinterpret_cast<uint64_t*>(c + hist_b + 2 * cnt_b);
     ws->chunks = (int)chunks;
     ws->words = (int)words;
+    ws->spc = (int)spc;
   }
   return hist_b + 2 * cnt_b + mask_b;
 }
@@ -349,6 +357,22 @@ __global__ void __launch_bounds__(256) sel_zero_kernel(uint32_t* p, int64_t coun
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) p[i] = 0u;
 }
 
+// The keys of this lane in its wave's span (key j0 + 64 i for i < kSelPer), all loads issued before any is used;
+// bit i of the result: the key exists and is a candidate.
+template <class KeyF>
+__device__ __forceinline__ uint32_t sel_load(const KeyF& kf, int64_t row, int j0, int n, const uint64_t* cm,
+                                             uint32_t (&key)[kSelPer]) {
+  uint32_t valid = 0;
+#pragma unroll
+  for (int i = 0; i < kSelPer; ++i) {
+    const int j = j0 + 64 * i;
+    const bool ok = j < n;
+    key[i] = ok ? kf(row, j) : 0u;
+    valid |= (uint32_t)(ok && sel_cand(cm, ok ? j : 0)) << i;
+  }
+  return valid;
+}
+
 // Pass `ps` of the histogram of selection `sel` (k of the candidates: every key, or the bits of selection cand_sel).
 template <class KeyF>
 __global__ void __launch_bounds__(kSelThreads) sel_hist_kernel(KeyF kf, int n, SelWs ws, int sel, int ps, uint32_t k,
@@ -363,25 +387,23 @@ __global__ void __launch_bounds__(kSelThreads) sel_hist_kernel(KeyF kf, int n, S
   sh.hist[tid] = 0u;
   __syncthreads();
   const int shift = 24 - 8 * ps;
-  const int j0 = blockIdx.x * kSelChunk + wv * kSelWaveSpan + lane;
-  for (int i = 0; i < kSelWaveSpan / 64; ++i) {
-    const int j = j0 + 64 * i;
-    const bool act = j < n && sel_cand(cm, j);
-    uint32_t d = 0;
-    bool m = false;
-    if (act) {
-      const uint32_t key = kf(row, j);
-      m = (key & pmask) == prefix;
-      d = (key >> shift) & 255u;
-    }
-    // lanes whose digit equals the first active lane's add as one (the leading byte is nearly constant per row)
-    const uint64_t active = __ballot(m);
-    if (active) {
-      const int leader = __ffsll((long long)active) - 1;
-      const uint32_t d0 = __shfl(d, leader, 64);
-      const uint64_t same = __ballot(m && d == d0);
-      if (lane == leader) atomicAdd(&sh.hist[d0], (uint32_t)__popcll(same));
-      else if (m && d != d0) atomicAdd(&sh.hist[d], 1u);
+  for (int sc = 0; sc < ws.spc; ++sc) {
+    uint32_t key[kSelPer];
+    const uint32_t valid =
+        sel_load(kf, row, (blockIdx.x * ws.spc + sc) * kSelChunk + wv * kSelWaveSpan + lane, n, cm, key);
+#pragma unroll
+    for (int i = 0; i < kSelPer; ++i) {
+      const bool m = ((valid >> i) & 1) && (key[i] & pmask) == prefix;
+      const uint32_t d = (key[i] >> shift) & 255u;
+      // lanes whose digit equals the first active lane's add as one (the leading byte is nearly constant per row)
+      const uint64_t active = __ballot(m);
+      if (active) {
+        const int leader = __ffsll((long long)active) - 1;
+        const uint32_t d0 = __shfl(d, leader, 64);
+        const uint64_t same = __ballot(m && d == d0);
+        if (lane == leader) atomicAdd(&sh.hist[d0], (uint32_t)__popcll(same));
+        else if (m && d != d0) atomicAdd(&sh.hist[d], 1u);
+      }
     }
   }
   __syncthreads();
@@ -399,10 +421,12 @@ __global__ void __launch_bounds__(kSelThreads) sel_eqcount_kernel(KeyF kf, int n
   uint32_t kstar, pmask, rem;
   sel_state(ws.hist + (row * kSelNSel + sel) * 1024, 4, k, kstar, pmask, rem, sh);
   uint32_t eq = 0;
-  const int j0 = blockIdx.x * kSelChunk + wv * kSelWaveSpan + lane;
-  for (int i = 0; i < kSelWaveSpan / 64; ++i) {
-    const int j = j0 + 64 * i;
-    if (j < n && sel_cand(cm, j)) eq += kf(row, j) == kstar;
+  for (int sc = 0; sc < ws.spc; ++sc) {
+    uint32_t key[kSelPer];
+    const uint32_t valid =
+        sel_load(kf, row, (blockIdx.x * ws.spc + sc) * kSelChunk + wv * kSelWaveSpan + lane, n, cm, key);
+#pragma unroll
+    for (int i = 0; i < kSelPer; ++i) eq += ((valid >> i) & 1) && key[i] == kstar;
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) eq += __shfl_xor(eq, off, 64);
@@ -441,40 +465,46 @@ __global__ void __launch_bounds__(kSelThreads) sel_mark_kernel(KeyF kf, int n, S
     sel_state(ws.hist + (row * kSelNSel + sel) * 1024, 4, k, kstar, pmask, rem, sh);
     eq_before = sel_block_sum(ws.eqcnt + (row * kSelNSel + sel) * ws.chunks, blockIdx.x, sh);
   }
-  // this lane's 64 keys: above K* / equal to K*, one bit per step
-  uint64_t gtb = 0, eqb = 0;
-  uint32_t weq_cnt = 0;
-  const int j0 = blockIdx.x * kSelChunk + wv * kSelWaveSpan + lane;
-  if (k > 0) {
-    for (int i = 0; i < kSelWaveSpan / 64; ++i) {
-      const int j = j0 + 64 * i;
-      if (j < n && sel_cand(cm, j)) {
-        const uint32_t key = kf(row, j);
-        gtb |= (uint64_t)(key > kstar) << i;
-        eqb |= (uint64_t)(key == kstar) << i;
+  // sub-chunk by sub-chunk, in key order: this lane's keys above / equal to K* (one bit per step), the equal ones'
+  // ranks counted over the earlier sub-chunks, waves and lanes
+  const uint64_t lt = (1ull << lane) - 1;
+  uint32_t rank_base = eq_before, taken = 0;
+  for (int sc = 0; sc < ws.spc; ++sc) {
+    const int js = (blockIdx.x * ws.spc + sc) * kSelChunk + wv * kSelWaveSpan;  // first key of this wave
+    uint32_t gtb = 0, eqb = 0, weq_cnt = 0;
+    if (k > 0) {
+      uint32_t key[kSelPer];
+      const uint32_t valid = sel_load(kf, row, js + lane, n, cm, key);
+#pragma unroll
+      for (int i = 0; i < kSelPer; ++i) {
+        const bool v = (valid >> i) & 1;
+        gtb |= (uint32_t)(v && key[i] > kstar) << i;
+        eqb |= (uint32_t)(v && key[i] == kstar) << i;
+      }
+      weq_cnt = __popc(eqb);
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) weq_cnt += __shfl_xor(weq_cnt, off, 64);
+    }
+    if (lane == 0) weq[wv] = weq_cnt;
+    __syncthreads();
+    uint32_t rank = rank_base;
+    for (int w2 = 0; w2 < wv; ++w2) rank += weq[w2];
+    rank_base += weq[0] + weq[1] + weq[2] + weq[3];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kSelPer; ++i) {
+      const int jw = js + 64 * i;  // first key of this step
+      if (jw < n) {
+        const bool e = (eqb >> i) & 1;
+        const uint64_t em = __ballot(e);
+        const uint32_t my_rank = rank + (uint32_t)__popcll(em & lt);
+        const bool take = ((gtb >> i) & 1) || (e && my_rank < rem);
+        const uint64_t tm = __ballot(take);
+        rank += (uint32_t)__popcll(em);
+        taken += (uint32_t)__popcll(tm);
+        if (lane == 0) out[jw >> 6] = tm;
       }
     }
-    weq_cnt = __popcll(eqb);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) weq_cnt += __shfl_xor(weq_cnt, off, 64);
-  }
-  if (lane == 0) weq[wv] = weq_cnt;
-  __syncthreads();
-  uint32_t rank = eq_before;
-  for (int w2 = 0; w2 < wv; ++w2) rank += weq[w2];
-  const uint64_t lt = (1ull << lane) - 1;
-  uint32_t taken = 0;
-  for (int i = 0; i < kSelWaveSpan / 64; ++i) {
-    const int jw = blockIdx.x * kSelChunk + wv * kSelWaveSpan + 64 * i;  // first key of this step
-    if (jw >= n) break;
-    const bool e = (eqb >> i) & 1;
-    const uint64_t em = __ballot(e);
-    const uint32_t my_rank = rank + (uint32_t)__popcll(em & lt);
-    const bool take = ((gtb >> i) & 1) || (e && my_rank < rem);
-    const uint64_t tm = __ballot(take);
-    rank += (uint32_t)__popcll(em);
-    taken += (uint32_t)__popcll(tm);
-    if (lane == 0) out[jw >> 6] = tm;
   }
   __syncthreads();
   if (lane == 0) sh.wsum[wv] = taken;
@@ -493,26 +523,33 @@ __global__ void __launch_bounds__(kSelThreads) sel_emit_kernel(int n, SelWs ws, 
   const uint64_t* mb = sel_b < 0 ? nullptr : ws.mask + (row * kSelNSel + sel_b) * ws.words;
   uint32_t base = sel_block_sum(ws.mcnt + (row * kSelNSel + sel_a) * ws.chunks, blockIdx.x, sh);
   if (sel_b >= 0) base += sel_block_sum(ws.mcnt + (row * kSelNSel + sel_b) * ws.chunks, blockIdx.x, sh);
-  const int w0 = (blockIdx.x * kSelChunk + wv * kSelWaveSpan) >> 6;  // first mask word of this wave
-  const int wend = min(ws.words, w0 + kSelWaveSpan / 64);
-  uint32_t tot = 0;
-  for (int w = w0 + lane; w < wend; w += 64) tot += __popcll(ma[w]) + (mb ? __popcll(mb[w]) : 0);
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) tot += __shfl_xor(tot, off, 64);
-  if (lane == 0) wtot[wv] = tot;
-  __syncthreads();
-  for (int w2 = 0; w2 < wv; ++w2) base += wtot[w2];
+  static_assert(kSelWaveSpan / 64 <= 64, "one mask word per lane");
   const uint64_t lt = (1ull << lane) - 1;
   int64_t* o = out + row * out_k;
-  for (int w = w0; w < wend; ++w) {
-    const uint64_t a = ma[w], b = mb ? mb[w] : 0ull;
-    if ((a | b) == 0) continue;
-    const int ba = (int)((a >> lane) & 1), bb = (int)((b >> lane) & 1);
-    uint32_t pos = base + (uint32_t)(__popcll(a & lt) + __popcll(b & lt));
-    const int64_t j = (int64_t)w * 64 + lane;
-    for (int r = 0; r < ba + bb; ++r, ++pos)
-      if (pos < (uint32_t)out_k) o[pos] = j;
-    base += (uint32_t)(__popcll(a) + __popcll(b));
+  for (int sc = 0; sc < ws.spc; ++sc) {
+    const int w0 = ((blockIdx.x * ws.spc + sc) * kSelChunk + wv * kSelWaveSpan) >> 6;  // first mask word of the wave
+    const int nwd = max(0, min(ws.words, w0 + kSelWaveSpan / 64) - w0);               // its words (one per lane)
+    const uint64_t my_a = lane < nwd ? ma[w0 + lane] : 0ull, my_b = mb && lane < nwd ? mb[w0 + lane] : 0ull;
+    uint32_t tot = __popcll(my_a) + __popcll(my_b);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) tot += __shfl_xor(tot, off, 64);
+    if (lane == 0) wtot[wv] = tot;
+    __syncthreads();
+    uint32_t pos0 = base;
+    for (int w2 = 0; w2 < wv; ++w2) pos0 += wtot[w2];
+    base += wtot[0] + wtot[1] + wtot[2] + wtot[3];
+    __syncthreads();
+    for (int i = 0; i < nwd; ++i) {
+      const int w = w0 + i;
+      const uint64_t a = __shfl(my_a, i, 64), b = __shfl(my_b, i, 64);
+      if ((a | b) == 0) continue;
+      const int ba = (int)((a >> lane) & 1), bb = (int)((b >> lane) & 1);
+      uint32_t pos = pos0 + (uint32_t)(__popcll(a & lt) + __popcll(b & lt));
+      const int64_t j = (int64_t)w * 64 + lane;
+      for (int r = 0; r < ba + bb; ++r, ++pos)
+        if (pos < (uint32_t)out_k) o[pos] = j;
+      pos0 += (uint32_t)(__popcll(a) + __popcll(b));
+    }
   }
 }
 

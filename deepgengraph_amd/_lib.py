@@ -48,6 +48,8 @@ SIGNATURES = {
     "dgg_attn_prefill_rope": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64p, _f32,
                                      _f32, _i64, _u32, _i32, _vp, _vp]),
     "dgg_rotary_cos_sin": (_i32, [_vp, _vp, _i64, _i64, _f32, _vp]),
+    "dgg_rotary_embedding": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _i32,
+                                    _vp]),
     "dgg_attn_colsum": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64p, _f32, _f32, _i64,
                                _u32, _i32, _vp]),
     "dgg_attn_colscore": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,

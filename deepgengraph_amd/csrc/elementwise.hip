@@ -366,6 +366,116 @@ int silu_dispatch(void* out, const void* in, int64_t rows, int64_t d, int64_t in
   return dgg::check_launch("silu_and_mul");
 }
 
+// ---------------------------------------------------------------------------------------------
+// Rotary with a (cos, sin) cache (csrc/pos_encoding.cu:7-61, host 152-178): row pos of the cache is
+// [cos (rot_dim/2) | sin (rot_dim/2)] in the storage type. NEOX pairs (i, i + rot_dim/2), GPT-J pairs (2i, 2i + 1),
+// i < rot_dim/2; the head dims past rot_dim are left as they are. The reference computes in its scalar_t: for the
+// 16-bit types each product and then the difference / sum is rounded to the storage type (c10 Half / BFloat16
+// operators compute in float and round), fp32 is plain fp32 arithmetic. One workgroup per token; VEC: 16-byte
+// chunks (NeoX: 8 pairs per item, GPT-J: 4 pairs), else one pair per item. A token whose position lies outside
+// [0, max_position) is left unchanged (nothing is read outside the cache).
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void rot_pair(float x, float y, float c, float s, float& xo, float& yo) {
+#pragma clang fp contract(off)
+  xo = round_t<T>(round_t<T>(x * c) - round_t<T>(y * s));
+  yo = round_t<T>(round_t<T>(y * c) + round_t<T>(x * s));
+}
+
+template <typename T, bool NEOX, bool VEC>
+__global__ void __launch_bounds__(256) rotary_cache_kernel(const int32_t* __restrict__ pos,
+                                                            typename T::scalar* __restrict__ q,
+                                                            typename T::scalar* __restrict__ k,
+                                                            const typename T::scalar* __restrict__ cache, int hq,
+                                                            int hk, int head_size, int rot_dim, int64_t max_pos,
+                                                            int64_t q_rs, int64_t k_rs) {
+  typedef typename T::scalar S;
+  const int64_t tok = blockIdx.x;
+  const int64_t p = pos[tok];
+  if (p < 0 || p >= max_pos) return;
+  const int embed = rot_dim / 2;
+  const S* cr = cache + p * rot_dim;  // cos at cr[i], sin at cr[embed + i]
+  auto head_base = [&](int h) -> S* {
+    return h < hq ? q + tok * q_rs + (int64_t)h * head_size : k + tok * k_rs + (int64_t)(h - hq) * head_size;
+  };
+  if constexpr (VEC) {
+    typedef typename VecOf<T>::type V;
+    constexpr int EPV = VecOf<T>::EPV;
+    if constexpr (NEOX) {
+      const int per_head = embed / EPV;  // 8-pair groups
+      const int items = (hq + hk) * per_head;
+      for (int it = threadIdx.x; it < items; it += blockDim.x) {
+        const int h = it / per_head, i0 = (it - h * per_head) * EPV;
+        S* base = head_base(h);
+        const V x = ld16<V>(base + i0), y = ld16<V>(base + embed + i0);
+        const V c = ld16<V>(cr + i0), sn = ld16<V>(cr + embed + i0);
+        V xo, yo;
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+          float a, b;
+          rot_pair<T>(to_f(x[e]), to_f(y[e]), to_f(c[e]), to_f(sn[e]), a, b);
+          xo[e] = to_s<S>(a);
+          yo[e] = to_s<S>(b);
+        }
+        st16<V>(base + i0, xo);
+        st16<V>(base + embed + i0, yo);
+      }
+    } else {
+      constexpr int PPC = EPV / 2;       // pairs per 16-byte chunk
+      const int per_head = rot_dim / EPV;  // chunks
+      const int items = (hq + hk) * per_head;
+      for (int it = threadIdx.x; it < items; it += blockDim.x) {
+        const int h = it / per_head, j = it - h * per_head;
+        S* base = head_base(h) + j * EPV;
+        const V xy = ld16<V>(base);
+        V o;
+#pragma unroll
+        for (int e = 0; e < PPC; ++e) {
+          float a, b;
+          const int r = j * PPC + e;
+          rot_pair<T>(to_f(xy[2 * e]), to_f(xy[2 * e + 1]), to_f(cr[r]), to_f(cr[embed + r]), a, b);
+          o[2 * e] = to_s<S>(a);
+          o[2 * e + 1] = to_s<S>(b);
+        }
+        st16<V>(base, o);
+      }
+    }
+  } else {
+    const int items = (hq + hk) * embed;
+    for (int it = threadIdx.x; it < items; it += blockDim.x) {
+      const int h = it / embed, r = it - h * embed;
+      S* base = head_base(h);
+      const int xi = NEOX ? r : 2 * r, yi = NEOX ? embed + r : 2 * r + 1;
+      float a, b;
+      rot_pair<T>(to_f(base[xi]), to_f(base[yi]), to_f(cr[r]), to_f(cr[embed + r]), a, b);
+      base[xi] = to_s<S>(a);
+      base[yi] = to_s<S>(b);
+    }
+  }
+}
+
+template <typename T>
+int rotary_cache_dispatch(const int32_t* pos, void* q, void* k, const void* cache, int64_t tokens, int64_t hq,
+                          int64_t hk, int64_t hs, int64_t rot_dim, int64_t max_pos, int64_t q_rs, int64_t k_rs,
+                          bool neox, hipStream_t st) {
+  typedef typename T::scalar S;
+  constexpr int EPV = VecOf<T>::EPV;
+  const bool vec = (neox ? (rot_dim / 2) % EPV == 0 : rot_dim % EPV == 0) && hs % EPV == 0 && q_rs % EPV == 0 &&
+                   (k == nullptr || k_rs % EPV == 0) && dgg::aligned16(q) && (k == nullptr || dgg::aligned16(k)) &&
+                   dgg::aligned16(cache) && rot_dim % EPV == 0;
+  const int64_t items = (hq + hk) * (vec ? (neox ? rot_dim / 2 / EPV : rot_dim / EPV) : rot_dim / 2);
+  int threads = (int)((items + 63) / 64 * 64);
+  threads = std::max(64, std::min(256, threads));
+  const dim3 grid((unsigned)tokens), block(threads);
+  auto args = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, block, 0, st, pos, (S*)q, (S*)k, (const S*)cache, (int)hq, (int)hk, (int)hs,
+                       (int)rot_dim, max_pos, q_rs, k_rs);
+  };
+  if (neox) vec ? args(rotary_cache_kernel<T, true, true>) : args(rotary_cache_kernel<T, true, false>);
+  else vec ? args(rotary_cache_kernel<T, false, true>) : args(rotary_cache_kernel<T, false, false>);
+  return dgg::check_launch("rotary_embedding");
+}
+
 template <typename T, int NV>
 void launch_rms_silu(int threads, unsigned silu_blocks, void* norm_out, const void* norm_in, const void* w,
                      int64_t norm_rows, int hidden, int64_t n_in_rs, int64_t n_out_rs, float eps, void* act_out,
@@ -494,6 +604,39 @@ extern "C" int dgg_silu_and_mul(void* out, const void* input, int64_t rows, int6
     case DGG_F16: return silu_dispatch<F16>(out, input, rows, d, in_row_stride, out_row_stride, st);
     case DGG_BF16: return silu_dispatch<BF16>(out, input, rows, d, in_row_stride, out_row_stride, st);
     default: return silu_dispatch<F32>(out, input, rows, d, in_row_stride, out_row_stride, st);
+  }
+}
+
+extern "C" int dgg_rotary_embedding(const int32_t* positions, void* query, void* key, int64_t tokens,
+                                    int64_t head_num, int64_t kv_head_num, int64_t head_size, int64_t q_row_stride,
+                                    int64_t k_row_stride, const void* cos_sin_cache, int64_t rot_dim,
+                                    int64_t max_position, int is_neox, int dtype, void* stream) {
+  DGG_REQUIRE(dgg::valid_dtype(dtype), DGG_ERR_DTYPE, "rotary_embedding: unsupported dtype code %d", dtype);
+  DGG_REQUIRE(tokens >= 0 && tokens <= 0x7fffffff, DGG_ERR_SHAPE, "rotary_embedding: bad token count %lld",
+              (long long)tokens);
+  DGG_REQUIRE(head_size > 0 && head_num >= 0 && kv_head_num >= 0 && head_num + kv_head_num < (1 << 20),
+              DGG_ERR_SHAPE, "rotary_embedding: bad head sizes");
+  DGG_REQUIRE(rot_dim >= 2 && rot_dim % 2 == 0 && rot_dim <= head_size, DGG_ERR_SHAPE,
+              "rotary_embedding: rot_dim %lld must be even and in [2, head_size = %lld]", (long long)rot_dim,
+              (long long)head_size);
+  DGG_REQUIRE(max_position >= 0, DGG_ERR_SHAPE, "rotary_embedding: max_position must be >= 0");
+  DGG_REQUIRE(q_row_stride >= head_num * head_size && (key == nullptr || k_row_stride >= kv_head_num * head_size),
+              DGG_ERR_STRIDE, "rotary_embedding: a row stride is smaller than the row");
+  if (key == nullptr) kv_head_num = 0;
+  if (tokens == 0 || head_num + kv_head_num == 0) return DGG_OK;
+  DGG_REQUIRE(positions && query && cos_sin_cache, DGG_ERR_NULL, "rotary_embedding: null pointer");
+  hipStream_t st = dgg::as_stream(stream);
+  const bool neox = is_neox != 0;
+  switch (dtype) {
+    case DGG_F16:
+      return rotary_cache_dispatch<F16>(positions, query, key, cos_sin_cache, tokens, head_num, kv_head_num, head_size,
+                                        rot_dim, max_position, q_row_stride, k_row_stride, neox, st);
+    case DGG_BF16:
+      return rotary_cache_dispatch<BF16>(positions, query, key, cos_sin_cache, tokens, head_num, kv_head_num,
+                                         head_size, rot_dim, max_position, q_row_stride, k_row_stride, neox, st);
+    default:
+      return rotary_cache_dispatch<F32>(positions, query, key, cos_sin_cache, tokens, head_num, kv_head_num, head_size,
+                                        rot_dim, max_position, q_row_stride, k_row_stride, neox, st);
   }
 }
 

@@ -138,3 +138,36 @@ def rotary_embedding_online(positions: torch.Tensor, query: torch.Tensor, key: t
     _lib.call("dgg_rotary_embedding_online", _lib.ptr(positions), _lib.ptr(query), _lib.ptr(key), tokens,
               width // head_size, hk, head_size, q_rs, k_rs, _lib.dtype_code(query.dtype), float(rope_theta),
               _lib.stream_handle(dev))
+
+
+def rotary_embedding(positions: torch.Tensor, query: torch.Tensor, key: torch.Tensor | None, head_size: int,
+                     cos_sin_cache: torch.Tensor, is_neox: bool) -> None:
+    """csrc/pos_encoding.cu:152-178 (the cos/sin-cache rotary, kernel pos_encoding.cu:7-61), in place on query
+    [..., Hq*head_size] and key [..., Hk*head_size]: cos_sin_cache [max_position, rot_dim] of the input dtype, row
+    p = [cos | sin]; is_neox pairs (i, i + rot_dim/2), else GPT-J pairs (2i, 2i+1); dims past rot_dim unchanged.
+    Products and results are rounded to the dtype as the reference's c10 Half / BFloat16 arithmetic rounds them.
+    A token whose position is outside [0, max_position) is left unchanged."""
+    dev = _lib.require_gpu(positions, query, key, cos_sin_cache)
+    if positions.dtype != torch.int32:
+        raise RuntimeError(f"rotary_embedding: positions must be int32 (got {positions.dtype})")
+    if cos_sin_cache.dtype != query.dtype or (key is not None and key.dtype != query.dtype):
+        raise RuntimeError("rotary_embedding: query, key and cos_sin_cache dtypes differ")
+    if cos_sin_cache.dim() != 2 or not cos_sin_cache.is_contiguous():
+        raise RuntimeError("rotary_embedding: cos_sin_cache must be a contiguous [max_position, rot_dim] tensor")
+    rot_dim = cos_sin_cache.shape[1]
+    width = query.shape[-1]
+    if head_size <= 0 or width % head_size:
+        raise RuntimeError(f"rotary_embedding: query width {width} is not a multiple of head_size {head_size}")
+    tokens = query.numel() // width if width else 0
+    if positions.numel() < tokens or not positions.is_contiguous():
+        raise RuntimeError(f"rotary_embedding: need a contiguous positions tensor with >= {tokens} entries")
+    _, q_rs = _rows(query, "rotary_embedding query")
+    hk, k_rs = 0, 0
+    if key is not None:
+        if key.shape[-1] % head_size or key.numel() // max(key.shape[-1], 1) != tokens:
+            raise RuntimeError("rotary_embedding: key width or token count does not match")
+        hk = key.shape[-1] // head_size
+        _, k_rs = _rows(key, "rotary_embedding key")
+    _lib.call("dgg_rotary_embedding", _lib.ptr(positions), _lib.ptr(query), _lib.ptr(key), tokens,
+              width // head_size, hk, head_size, q_rs, k_rs, _lib.ptr(cos_sin_cache), rot_dim, cos_sin_cache.shape[0],
+              1 if is_neox else 0, _lib.dtype_code(query.dtype), _lib.stream_handle(dev))

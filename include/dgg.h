@@ -95,6 +95,18 @@ int dgg_rms_norm_silu_and_mul(void* norm_out, const void* norm_in, const void* w
 int dgg_rotary_embedding_online(const int32_t* positions, void* query, void* key, int64_t tokens,
                                 int64_t head_num, int64_t kv_head_num, int64_t head_dim, int64_t q_row_stride,
                                 int64_t k_row_stride, int dtype, float rope_theta, void* stream);
+/* csrc/pos_encoding.cu:152-178 rotary_embedding(positions, query, key, head_size, cos_sin_cache, is_neox) (the kernel
+ * of pos_encoding.cu:7-61; not exported by the reference's ffi.cpp): in place on query [tokens, head_num*head_size]
+ * and key [tokens, kv_head_num*head_size] (row strides as dgg_rotary_embedding_online; key may be NULL), with
+ * cos_sin_cache [max_position, rot_dim] of the input dtype, row p = [cos (rot_dim/2) | sin (rot_dim/2)]. is_neox:
+ * pairs (i, i + rot_dim/2), else GPT-J pairs (2i, 2i+1), i < rot_dim/2; dims past rot_dim are untouched.
+ * x' = x*cos - y*sin, y' = y*cos + x*sin with the reference's rounding: for f16/bf16 each product and the result are
+ * rounded to the dtype (c10 Half / BFloat16 arithmetic). A token whose position lies outside [0, max_position) is
+ * left unchanged (the reference would read outside the cache). rot_dim even, 2 <= rot_dim <= head_size. */
+int dgg_rotary_embedding(const int32_t* positions, void* query, void* key, int64_t tokens, int64_t head_num,
+                         int64_t kv_head_num, int64_t head_size, int64_t q_row_stride, int64_t k_row_stride,
+                         const void* cos_sin_cache, int64_t rot_dim, int64_t max_position, int is_neox, int dtype,
+                         void* stream);
 /* The (cos, sin) table of the online rotary for dgg_attn_prefill_rope (no counterpart in the reference; the values
  * are those rotary_embedding_online computes, pos_encoding.cu:83-86): cos_sin fp32 [tokens, head_dim], row t =
  * cos(pos[t] / theta^(2i/head_dim)) for i < head_dim/2, then the sines. */

@@ -60,3 +60,34 @@ def rotary_embedding_online(positions, query, key, head_size: int, rope_theta: f
         return o.to(t.dtype).reshape(t.shape)
 
     return rot(query), rot(key)
+
+
+def rotary_embedding(positions, query, key, head_size: int, cos_sin_cache, is_neox: bool):
+    """csrc/pos_encoding.cu:7-61, 152-178, out of place: cos_sin_cache [max_position, rot_dim] of the input dtype,
+    row p = [cos (rot_dim/2) | sin (rot_dim/2)]; pairs (i, i + rot_dim/2) (is_neox) or (2i, 2i+1) for i < rot_dim/2;
+    x' = x*cos - y*sin, y' = y*cos + x*sin in the reference's scalar_t arithmetic: for 16-bit types each product and
+    the result rounded to the dtype (c10 Half / BFloat16 operators compute in float and round), fp32 plain. Head
+    dims past rot_dim are unchanged. Returns (query_out, key_out)."""
+    rot_dim = cos_sin_cache.shape[1]
+    embed = rot_dim // 2
+    cache = cos_sin_cache[positions.reshape(-1).long()]
+    cos, sin = cache[:, :embed].unsqueeze(1), cache[:, embed:].unsqueeze(1)
+
+    def mul(a, b):
+        return (a.float() * b.float()).to(a.dtype)
+
+    def rot(t):
+        if t is None:
+            return None
+        T = t.shape[0]
+        x = t.reshape(T, -1, head_size).clone()
+        if is_neox:
+            xs, ys = slice(0, embed), slice(embed, rot_dim)
+        else:
+            xs, ys = slice(0, rot_dim, 2), slice(1, rot_dim, 2)
+        a, b = x[..., xs].clone(), x[..., ys].clone()
+        x[..., xs] = (mul(a, cos).float() - mul(b, sin).float()).to(t.dtype)
+        x[..., ys] = (mul(b, cos).float() + mul(a, sin).float()).to(t.dtype)
+        return x.reshape(t.shape)
+
+    return rot(query), rot(key)

@@ -151,6 +151,16 @@ def test_elementwise_validation(lib):
     assert lib.dgg_rotary_embedding_online(None, FAKE, FAKE, 8, 4, 4, 128, 512, 512, 1, 1e4, None) == E_NULL
 
 
+def test_rotary_cache_validation(lib):
+    # positions, query, key, tokens, hq, hk, head_size, q_rs, k_rs, cache, rot_dim, max_position, is_neox, dtype
+    assert lib.dgg_rotary_embedding(FAKE, FAKE, FAKE, 8, 4, 4, 128, 512, 512, FAKE, 128, 100, 1, 5, None) == E_DTYPE
+    assert lib.dgg_rotary_embedding(FAKE, FAKE, FAKE, 8, 4, 4, 128, 512, 512, FAKE, 130, 100, 1, 1, None) == E_SHAPE
+    assert lib.dgg_rotary_embedding(FAKE, FAKE, FAKE, 8, 4, 4, 128, 512, 512, FAKE, 63, 100, 0, 1, None) == E_SHAPE
+    assert lib.dgg_rotary_embedding(FAKE, FAKE, FAKE, 8, 4, 4, 128, 500, 512, FAKE, 64, 100, 0, 1, None) == E_STRIDE
+    assert lib.dgg_rotary_embedding(FAKE, FAKE, FAKE, 8, 4, 4, 128, 512, 512, None, 64, 100, 0, 1, None) == E_NULL
+    assert lib.dgg_rotary_embedding(None, None, None, 0, 4, 4, 128, 512, 512, None, 64, 100, 0, 1, None) == OK
+
+
 def test_topk_validation(lib):
     assert lib.dgg_topk_indices(FAKE, 4, 100, 0, FAKE, None) == E_SHAPE
     assert lib.dgg_topk_indices(FAKE, 4, 100, 101, FAKE, None) == E_SHAPE

@@ -188,3 +188,49 @@ def test_wrapper_errors(gpu):
         ops.fused_add_rms_norm(h, h.clone(), torch.ones(128, dtype=torch.float16, device=gpu)[::2], 1e-6)
     with pytest.raises(RuntimeError, match="must be positive"):
         ops.rotary_embedding_online(torch.zeros(4, dtype=torch.int32, device=gpu), h, None, 0, 1e4)
+
+
+@pytest.mark.parametrize("tokens,hq,hk,hs,rot,dtype,neox,pad", [
+    (4096, 32, 32, 128, 128, torch.bfloat16, True, 0),    # config-2 sized, NeoX, full rotary
+    (300, 8, 2, 128, 128, torch.float16, False, 0),       # GPT-J pairs
+    (77, 4, 4, 256, 64, torch.bfloat16, False, 0),        # partial rotary (GPT-J style rot_dim 64 of 256)
+    (50, 3, 1, 64, 48, torch.float16, True, 8),           # NeoX partial, padded rows
+    (33, 2, 2, 96, 40, torch.float16, True, 0),           # rot_dim/2 not a multiple of 8: scalar path
+    (20, 2, 1, 64, 64, torch.float32, False, 4),
+])
+def test_rotary_cos_sin_cache(gpu, tokens, hq, hk, hs, rot, dtype, neox, pad):
+    # csrc/pos_encoding.cu:7-61 (rotary_embedding with a cos/sin cache): bit-identical to the oracle in 16 bits (the
+    # products are exact in fp32 and every rounding point is the reference's), fp32 within 1e-6
+    g = torch.Generator().manual_seed(tokens + rot)
+    max_pos = 5000
+    ang = torch.rand(max_pos, rot // 2, generator=g, dtype=torch.float64) * 50.0
+    cache = torch.cat([ang.cos(), ang.sin()], dim=1).to(dtype)
+    pos = torch.randint(0, max_pos, (tokens,), generator=g, dtype=torch.int32)
+    q = _randn((tokens, hq * hs + pad), dtype, 31, 2.0)
+    k = _randn((tokens, hk * hs + pad), dtype, 32, 2.0)
+    ref_q, ref_k = oe.rotary_embedding(pos, q[:, : hq * hs], k[:, : hk * hs], hs, cache, neox)
+    qg, kg = q.to(gpu), k.to(gpu)
+    ops.rotary_embedding(pos.to(gpu), qg[:, : hq * hs], kg[:, : hk * hs], hs, cache.to(gpu), neox)
+    what = f"rotary cache T{tokens} {hq}/{hk} hs{hs} rot{rot} {dtype} neox={neox}"
+    if dtype == torch.float32:
+        assert_close(qg[:, : hq * hs].cpu(), ref_q, 1e-6, 1e-6, what + " q")
+        assert_close(kg[:, : hk * hs].cpu(), ref_k, 1e-6, 1e-6, what + " k")
+    else:
+        assert torch.equal(qg[:, : hq * hs].cpu(), ref_q), what + " q"
+        assert torch.equal(kg[:, : hk * hs].cpu(), ref_k), what + " k"
+    assert torch.equal(qg[:, hq * hs:].cpu(), q[:, hq * hs:]), "row padding must be untouched"
+
+
+def test_rotary_cos_sin_cache_positions_outside_the_cache(gpu):
+    # a position outside [0, max_position) leaves its token unchanged (nothing is read outside the cache); key may be
+    # omitted
+    cache = torch.cat([torch.full((4, 8), 0.5), torch.full((4, 8), 0.25)], dim=1).half()
+    q = _randn((5, 2 * 16), torch.float16, 40)
+    pos = torch.tensor([0, 3, 4, -1, 2], dtype=torch.int32)
+    qg = q.to(gpu)
+    ops.rotary_embedding(pos.to(gpu), qg, None, 16, cache.to(gpu), True)
+    got = qg.cpu()
+    ok = torch.tensor([0, 1, 4])
+    ref, _ = oe.rotary_embedding(pos[ok], q[ok], None, 16, cache, True)
+    assert torch.equal(got[ok], ref)
+    assert torch.equal(got[2:4], q[2:4])

@@ -481,3 +481,83 @@ def test_nonzero_matches_loops():
     want = [[b, h, j] for b in range(2) for h in range(3) for j in range(17) if bool(x[b, h, j])]
     assert got.dtype == torch.int64 and got.tolist() == want
     assert osel.nonzero(torch.zeros(4, 5, dtype=torch.bool)).shape == (0, 2)
+
+
+def _rope_cache(max_pos, rot_dim, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    ang = torch.rand(max_pos, rot_dim // 2, generator=g, dtype=torch.float64) * 40.0
+    return torch.cat([ang.cos(), ang.sin()], dim=1).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_rotary_cache_rounding_points_against_torch_16bit_arithmetic(dtype):
+    # the reference computes in its scalar_t: c10 Half / BFloat16 operators compute in float and round each product and
+    # the result; torch's own 16-bit CPU tensor arithmetic does the same, so x*c - y*s written with 16-bit tensors
+    # must give the oracle's bits for both pairings and a partial rot_dim
+    g = torch.Generator().manual_seed(3)
+    T, H, hs, rot = 7, 3, 64, 48
+    cache = _rope_cache(50, rot, dtype, 4)
+    pos = torch.randint(0, 50, (T,), generator=g, dtype=torch.int32)
+    q = (torch.randn(T, H * hs, generator=g) * 3).to(dtype)
+    for neox in (True, False):
+        got, _ = oe.rotary_embedding(pos, q, None, hs, cache, neox)
+        x = q.reshape(T, H, hs)
+        c = cache[pos.long(), : rot // 2].unsqueeze(1)
+        s = cache[pos.long(), rot // 2:].unsqueeze(1)
+        a, b = (x[..., : rot // 2], x[..., rot // 2: rot]) if neox else (x[..., 0:rot:2], x[..., 1:rot:2])
+        want = x.clone()
+        if neox:
+            want[..., : rot // 2], want[..., rot // 2: rot] = a * c - b * s, b * c + a * s
+        else:
+            want[..., 0:rot:2], want[..., 1:rot:2] = a * c - b * s, b * c + a * s
+        assert torch.equal(got.reshape(T, H, hs), want), f"neox={neox}"
+        assert torch.equal(got.reshape(T, H, hs)[..., rot:], x[..., rot:]), "dims past rot_dim must be unchanged"
+    # and the roundings are observable: a single rounding of x*c - y*s differs on these inputs
+    single = (a.float() * c.float() - b.float() * s.float()).to(dtype)
+    assert not torch.equal(single, (a * c - b * s)), "inputs must make the product roundings observable"
+
+
+def test_rotary_cache_pairing_and_layout():
+    # NeoX with the cache of the online angles equals the online rotary (fp32); GPT-J on interleaved pairs equals NeoX on
+    # the same pairs laid out as halves; an identity cache (cos 1, sin 0) changes nothing
+    T, H, hs = 5, 2, 128
+    g = torch.Generator().manual_seed(8)
+    pos = torch.randint(0, 3000, (T,), generator=g, dtype=torch.int32)
+    q = torch.randn(T, H * hs, generator=g)
+    c, s = oe.rotary_cos_sin(torch.arange(3000, dtype=torch.int32), hs, 10000.0)
+    cache = torch.cat([c, s], dim=1)
+    got, _ = oe.rotary_embedding(pos, q, None, hs, cache, True)
+    ref, _ = oe.rotary_embedding_online(pos, q, None, hs, 10000.0)
+    assert_close(got, ref, 2e-6, 2e-6, "neox cache vs online")
+    x = q.reshape(T, H, hs)
+    inter = torch.stack([x[..., : hs // 2], x[..., hs // 2:]], dim=-1).reshape(T, H * hs)  # (x_i, y_i) adjacent
+    gj, _ = oe.rotary_embedding(pos, inter, None, hs, cache, False)
+    gj = gj.reshape(T, H, hs // 2, 2)
+    assert torch.equal(torch.cat([gj[..., 0], gj[..., 1]], dim=-1), got.reshape(T, H, hs))
+    ident = torch.cat([torch.ones(10, 32), torch.zeros(10, 32)], dim=1).half()
+    qh = q.half()
+    for neox in (True, False):
+        assert torch.equal(oe.rotary_embedding(pos % 10, qh, None, hs, ident, neox)[0], qh)
+
+
+def test_rotary_cache_brute_force_fp32():
+    # float64 loops over every pair against the fp32 oracle
+    T, H, hs, rot = 3, 2, 32, 16
+    g = torch.Generator().manual_seed(9)
+    pos = torch.randint(0, 20, (T,), generator=g, dtype=torch.int32)
+    q = torch.randn(T, H * hs, generator=g)
+    k = torch.randn(T, 1 * hs, generator=g)
+    cache = _rope_cache(20, rot, torch.float32, 10)
+    for neox in (True, False):
+        gq, gk = oe.rotary_embedding(pos, q, k, hs, cache, neox)
+        for t_in, t_out in ((q, gq), (k, gk)):
+            want = t_in.double().clone()
+            for t in range(T):
+                cr = cache[int(pos[t])].double()
+                for h in range(t_in.shape[1] // hs):
+                    for i in range(rot // 2):
+                        xi, yi = (i, rot // 2 + i) if neox else (2 * i, 2 * i + 1)
+                        x, y = t_in[t, h * hs + xi].double(), t_in[t, h * hs + yi].double()
+                        want[t, h * hs + xi] = x * cr[i] - y * cr[rot // 2 + i]
+                        want[t, h * hs + yi] = y * cr[i] + x * cr[rot // 2 + i]
+            assert_close(t_out, want, 1e-6, 1e-6, f"brute force neox={neox}")

@@ -52,6 +52,34 @@ def _run_both(dev, B, H, Hkv, L, D, dtype, splits, seed):
     assert torch.isfinite(o_na.float()).all()
 
 
+def test_scratch_is_taken_only_by_a_no_alloc_call(gpu):
+    # the 96 MiB array lives in its own code object, which the runtime loads onto a device when the no-alloc entry
+    # point is first used there: the other decode calls do not take it (this test must be the process's first no-alloc
+    # call, so it comes first in the file and no other test file calls the entry point)
+    lib = _lib.load()
+    B, H, L, D = 2, 4, 1000, 128
+    q, k, v = _inputs(B, H, H, L, D, torch.float16, 7, gpu)
+    o = torch.empty_like(q)
+    need = lib.dgg_attn_decode_workspace_bytes(B, H, D, 8)
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+    stream = _lib.stream_handle(gpu)
+    scale = ctypes.c_float(D ** -0.5)
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    rc = lib.dgg_attn_decode(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), None, _lib.ptr(ws), need, B, H, H, L,
+                             D, _strides(q, k, v, o), 8, scale, _lib.DGG_F16, stream)
+    assert rc == 0, lib.dgg_last_error()
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    rc = lib.dgg_attn_decode_noalloc(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), None, B, H, H, L, D,
+                                     _strides(q, k, v, o), 8, scale, _lib.DGG_F16, stream)
+    assert rc == 0, lib.dgg_last_error()
+    torch.cuda.synchronize()
+    free2 = torch.cuda.mem_get_info()[0]
+    assert free0 - free1 < SCRATCH_BYTES // 2, f"a workspace decode took {(free0 - free1) >> 20} MiB"
+    assert free1 - free2 >= SCRATCH_BYTES, f"the first no-alloc call took only {(free1 - free2) >> 20} MiB"
+
+
 def test_noalloc_decode_matches_workspace_entry_point(gpu):
     # a large call that fills most of the scratch, then a smaller one that reuses (and must not read) its contents
     _run_both(gpu, 16, 32, 8, 8192, 128, torch.float16, 64, seed=1)   # 17.0 MB of partials

@@ -101,6 +101,16 @@ template <typename V>
 __device__ __forceinline__ void st16(void* p, V v) {
   *reinterpret_cast<V*>(p) = v;
 }
+// The same with the non-temporal hint, for data a kernel reads or writes once (a streamed row, an output nobody
+// re-reads in the same kernel).
+template <typename V>
+__device__ __forceinline__ V ld16_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const V*>(p));
+}
+template <typename V>
+__device__ __forceinline__ void st16_nt(void* p, V v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<V*>(p));
+}
 
 // Pointers in the global address space (loads through them are global_load_*, never flat_load_*).
 typedef const char __attribute__((address_space(1)))* gptr;

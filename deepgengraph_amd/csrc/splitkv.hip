@@ -120,13 +120,15 @@ attn_splitkv_kernel(SplitParams sp) {
   const S* kp = static_cast<const S*>(p.k) + b * p.k_sb + (int64_t)hk * p.k_sh + c0 * 8;
   const S* vp = static_cast<const S*>(p.v) + b * p.v_sb + (int64_t)hk * p.v_sh + c0 * 8;
   V8 kreg[CPT], vreg[CPT];
-  // Rows past the split's end re-read its last key (masked below, finite: contributes exactly 0).
+  // Rows past the split's end re-read its last key (masked below, finite: contributes exactly 0). Each K / V row is
+  // read once, so the loads are non-temporal: measured at q_len 4 over 32K keys, 90.3-90.6 against 101.3-101.5 us
+  // with ordinary loads (the stream alone, without the tile compute, runs the same times: the loop is bound by it).
   auto load = [&](int t) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int key = min(k0 + t * BN + i * RPI + row0, k1 - 1);
-      kreg[i] = ld16<V8>(kp + (int64_t)key * p.k_ss);
-      vreg[i] = ld16<V8>(vp + (int64_t)key * p.v_ss);
+      kreg[i] = __builtin_nontemporal_load(reinterpret_cast<const V8*>(kp + (int64_t)key * p.k_ss));
+      vreg[i] = __builtin_nontemporal_load(reinterpret_cast<const V8*>(vp + (int64_t)key * p.v_ss));
     }
   };
   auto store = [&]() {

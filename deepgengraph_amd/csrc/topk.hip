@@ -60,9 +60,11 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* w
 // largest keys, equal keys lowest index first, and returns the calling thread's take bits. k must not exceed the
 // number of candidates. Histograms are per wave (no atomics shared across waves); the digit of each pass is found
 // by a 256-thread suffix scan over the bins. Every thread of the block calls this with the same k.
+// The digit passes of radix_take: kstar = K*, the k-th largest candidate key (k >= 1), and `remaining` = the number
+// of candidates equal to K* among the k.
 template <int PER>
-__device__ uint64_t radix_take(const uint32_t (&key)[PER], uint64_t cand, uint32_t k, TopkShared& sh) {
-  if (k == 0) return 0;
+__device__ void radix_kstar(const uint32_t (&key)[PER], uint64_t cand, uint32_t k, TopkShared& sh, uint32_t& kstar,
+                            uint32_t& remaining_out) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   uint32_t prefix = 0, pmask = 0, remaining = k;
   for (int shift = 24; shift >= 0; shift -= 8) {
@@ -120,6 +122,15 @@ __device__ uint64_t radix_take(const uint32_t (&key)[PER], uint64_t cand, uint32
     pmask |= 255u << shift;
     remaining = sh.sel_remaining;
   }
+  kstar = prefix;
+  remaining_out = remaining;
+}
+
+template <int PER>
+__device__ uint64_t radix_take(const uint32_t (&key)[PER], uint64_t cand, uint32_t k, TopkShared& sh) {
+  if (k == 0) return 0;
+  uint32_t prefix, remaining;
+  radix_kstar<PER>(key, cand, k, sh, prefix, remaining);
   // prefix = K*; `remaining` candidates equal to K* are still to be taken, lowest index first.
   uint32_t eq = 0;
 #pragma unroll
@@ -151,6 +162,18 @@ __device__ __forceinline__ void write_taken(uint64_t a, uint64_t b, int seg0, in
       if (pos < total) o[pos++] = seg0 + j;
     a &= ~low;
     b &= ~low;
+  }
+}
+
+// As write_taken for one mask, writing idx[seg0 + j] in place of seg0 + j (positions ascending).
+__device__ __forceinline__ void write_taken_gather(uint64_t a, int seg0, const int* __restrict__ idx,
+                                                   int64_t* __restrict__ o, uint32_t total, TopkShared& sh) {
+  uint32_t tot;
+  uint32_t pos = block_exclusive_scan(__popcll(a), sh.wsum, tot);
+  while (a) {
+    const int j = __ffsll((long long)a) - 1;
+    if (pos < total) o[pos++] = idx[seg0 + j];
+    a &= a - 1;
   }
 }
 
@@ -226,15 +249,23 @@ __global__ void __launch_bounds__(kTopkThreads) roco_select_kernel(const float* 
 // workgroups per row, in passes through a caller-provided workspace. A row is cut into chunks of kSelChunk keys, one
 // 256-thread workgroup per (chunk, row); wave w of a chunk owns its contiguous kSelWaveSpan keys, 64 at a time
 // (lane l on key 64i + l), so a 64-bit ballot is one aligned word of a bit mask.
-//   1. four histogram passes: pass p counts the candidates whose key matches the digits chosen so far into 256 bins
+//   1. two histogram passes: pass p counts the candidates whose key matches the digits chosen so far into 256 bins
 //      of its byte (LDS, then one global atomic per bin and workgroup); every workgroup of the next pass re-derives
 //      the chosen digits from the finished histograms (a 256-bin suffix scan per pass);
-//   2. per chunk, the number of candidates whose key equals K*, the k-th largest key;
-//   3. the selection as a bit mask: every candidate above K*, and candidates equal to K* while their rank among the
-//      equal ones (counted over the earlier chunks, the earlier waves of the chunk and the earlier lanes) is below
-//      the number still to take, i.e. lowest index first; plus the mask's population per chunk;
-//   4. the indices of one or two masks in ascending order (an index in both written twice), each chunk at the sum of
+//   2. the split at the 16-bit prefix P of K*, the k-th largest key: every candidate whose top 16 bits exceed P is
+//      taken, its bit written straight into the selection's mask; the candidates whose top 16 bits equal P, the
+//      only keys the remaining passes look at, go into a second bit mask (the prefix mask), and their third byte
+//      into histogram pass 2;
+//   3. histogram pass 3 over the prefix mask's keys;
+//   4. per chunk, the number of prefix-mask keys equal to K*;
+//   5. the rest of the selection: prefix-mask keys above K*, and those equal to K* while their rank among the equal
+//      ones (counted over the earlier chunks, the earlier waves of the chunk and the earlier lanes) is below the
+//      number still to take, i.e. lowest index first, OR'ed into the mask words of step 2; plus the mask's
+//      population per chunk;
+//   6. the indices of one or two masks in ascending order (an index in both written twice), each chunk at the sum of
 //      the populations before it.
+// Steps 1 and 2 read every key (three reads of the row); steps 3-5 load only the keys of mask words that hold a
+// prefix-mask bit, which for scores in general is a small share of the row (all of it when every key is equal).
 // RoCo chains three selections: `recent` (largest std), `other` (smallest std), `pick` (largest mean among the
 // candidates of `other`'s mask), then writes pick and recent.
 // ------------------------------------------------------------------------------------------------
@@ -244,12 +275,21 @@ constexpr int kSelWaveSpan = 64 * kSelPer;                  // keys per wave per
 constexpr int kSelChunk = kSelWaveSpan * (kSelThreads / 64);  // keys per workgroup
 constexpr int kSelMaxN = 1 << 26;
 constexpr int kSelNSel = 3;                                 // selections a workspace holds (RoCo's three)
+// Two-stage top-k (small k): each 1024-thread workgroup takes the k largest of its kSel2Chunk keys, then one workgroup
+// per row selects among the chunks' candidates (at most kSel2MaxCand, held in registers by topk's kernels). (32 keys
+// per lane instead of 16 spills: 124 VGPRs and 164 SGPRs.)
+constexpr int kSel2Per = 16;                                // keys per lane in the first stage
+constexpr int kSel2Chunk = 64 * kSel2Per * kTopkWaves;      // keys per workgroup
+constexpr int kSel2MaxCand = 64 * kTopkThreads;             // candidates per row
 
 struct SelWs {
   uint32_t* hist;   // [rows][kSelNSel][4][256]
   uint32_t* eqcnt;  // [rows][kSelNSel][chunks]
   uint32_t* mcnt;   // [rows][kSelNSel][chunks]
   uint64_t* mask;   // [rows][kSelNSel][words]
+  uint64_t* pre;    // [rows][words]: the prefix mask of the selection in progress
+  uint32_t* ckey;   // [rows][kSel2MaxCand]: two-stage candidates (top-k with chunks * k <= kSel2MaxCand)
+  int* cidx;        // [rows][kSel2MaxCand]
   int chunks, words;
   int spc;          // kSelChunk-key sub-chunks per workgroup (a chunk is spc * kSelChunk keys)
 };
@@ -267,46 +307,56 @@ inline int64_t sel_layout(int64_t rows, int64_t n, void* base, SelWs* ws) {
   const int64_t hist_b = sel_align(rows * kSelNSel * 1024 * 4);
   const int64_t cnt_b = sel_align(rows * kSelNSel * chunks * 4);
   const int64_t mask_b = sel_align(rows * kSelNSel * words * 8);
+  const int64_t pre_b = sel_align(rows * words * 8);
+  const int64_t cand_b = sel_align(rows * (int64_t)kSel2MaxCand * 4);
   if (ws != nullptr) {
     char* c = static_cast<char*>(base);
     ws->hist = reinterpret_cast<uint32_t*>(c);
     ws->eqcnt = reinterpret_cast<uint32_t*>(c + hist_b);
     ws->mcnt = reinterpret_cast<uint32_t*>(c + hist_b + cnt_b);
     ws->mask = reinterpret_cast<uint64_t*>(c + hist_b + 2 * cnt_b);
+    ws->pre = reinterpret_cast<uint64_t*>(c + hist_b + 2 * cnt_b + mask_b);
+    ws->ckey = reinterpret_cast<uint32_t*>(c + hist_b + 2 * cnt_b + mask_b + pre_b);
+    ws->cidx = reinterpret_cast<int*>(c + hist_b + 2 * cnt_b + mask_b + pre_b + cand_b);
     ws->chunks = (int)chunks;
     ws->words = (int)words;
     ws->spc = (int)spc;
   }
-  return hist_b + 2 * cnt_b + mask_b;
+  return hist_b + 2 * cnt_b + mask_b + pre_b + 2 * cand_b;
 }
 
-// Key sources: element j of row `row` as an order key (larger = taken first).
+// Key sources: element j of row `row` as an order key (larger = taken first), in two steps: load() reads what the
+// key is made from, key() forms it (so that a caller can issue every load before it waits for any).
 struct KeyScores {  // topk_kernel's key: the score, complemented for the smallest-first direction
+  typedef float raw_t;
   const float* x;
   int n, largest;
-  __device__ __forceinline__ uint32_t operator()(int64_t row, int j) const {
-    const uint32_t k = order_key(x[row * n + j]);
+  __device__ __forceinline__ raw_t load(int64_t row, int j) const { return x[row * n + j]; }
+  __device__ __forceinline__ uint32_t key(raw_t v) const {
+    const uint32_t k = order_key(v);
     return largest ? k : ~k;
   }
 };
 struct KeyStd {  // roco_select_kernel's std key (complemented: the smallest first)
+  typedef f32x2 raw_t;
   const float* s1;
   const float* s2;
   int n;
   float rcp;
   int complement;
-  __device__ __forceinline__ uint32_t operator()(int64_t row, int j) const {
-    const uint32_t k = order_key(roco_std(s1[row * n + j], s2[row * n + j], rcp));
+  __device__ __forceinline__ raw_t load(int64_t row, int j) const { return f32x2{s1[row * n + j], s2[row * n + j]}; }
+  __device__ __forceinline__ uint32_t key(raw_t v) const {
+    const uint32_t k = order_key(roco_std(v[0], v[1], rcp));
     return complement ? ~k : k;
   }
 };
 struct KeyMean {  // roco_select_kernel's third key: roco_score / q_len
+  typedef float raw_t;
   const float* s1;
   int n;
   float rcp;
-  __device__ __forceinline__ uint32_t operator()(int64_t row, int j) const {
-    return order_key(roco_mean(s1[row * n + j], rcp));
-  }
+  __device__ __forceinline__ raw_t load(int64_t row, int j) const { return s1[row * n + j]; }
+  __device__ __forceinline__ uint32_t key(raw_t v) const { return order_key(roco_mean(v, rcp)); }
 };
 
 struct SelShared {
@@ -349,28 +399,71 @@ __device__ void sel_state(const uint32_t* H, int np, uint32_t k, uint32_t& prefi
   }
 }
 
-__device__ __forceinline__ bool sel_cand(const uint64_t* cmask, int j) {
-  return cmask == nullptr || ((cmask[j >> 6] >> (j & 63)) & 1);
+// Candidate sets of a pass: every key (kSelAll), the prefix mask (kSelPrefix), or the mask of an earlier selection.
+constexpr int kSelAll = -1, kSelPrefix = -2;
+__device__ __forceinline__ const uint64_t* sel_cmask(const SelWs& ws, int64_t row, int cand) {
+  if (cand == kSelPrefix) return ws.pre + row * ws.words;
+  return cand < 0 ? nullptr : ws.mask + (row * kSelNSel + cand) * ws.words;
 }
 
 __global__ void __launch_bounds__(256) sel_zero_kernel(uint32_t* p, int64_t count) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) p[i] = 0u;
 }
 
-// The keys of this lane in its wave's span (key j0 + 64 i for i < kSelPer), all loads issued before any is used;
-// bit i of the result: the key exists and is a candidate.
+// The keys of this lane in its wave's span (key j0 + 64 i for i < kSelPer, j0 - lane a multiple of 64), all loads
+// issued before any is used; bit i of the result: the key exists and is a candidate. With a candidate mask, step i
+// covers exactly mask word (j0 - lane) / 64 + i: its words are loaded first (one per lane), a step whose word is zero
+// issues no load, and only the lanes of candidates load their key.
 template <class KeyF>
 __device__ __forceinline__ uint32_t sel_load(const KeyF& kf, int64_t row, int j0, int n, const uint64_t* cm,
                                              uint32_t (&key)[kSelPer]) {
   uint32_t valid = 0;
+  if (cm == nullptr) {
+#pragma unroll
+    for (int i = 0; i < kSelPer; ++i) {
+      const int j = j0 + 64 * i;
+      const bool ok = j < n;
+      key[i] = ok ? kf.key(kf.load(row, j)) : 0u;
+      valid |= (uint32_t)ok << i;
+    }
+    return valid;
+  }
+  const int lane = threadIdx.x & 63;
+  const int w0 = (j0 - lane) >> 6, nwords = (n + 63) >> 6;
+  const uint64_t mine = lane < kSelPer && w0 + lane < nwords ? cm[w0 + lane] : 0ull;
+  static_assert(kSelPer <= 64, "one candidate word per lane");
+  typename KeyF::raw_t raw[kSelPer];
 #pragma unroll
   for (int i = 0; i < kSelPer; ++i) {
-    const int j = j0 + 64 * i;
-    const bool ok = j < n;
-    key[i] = ok ? kf(row, j) : 0u;
-    valid |= (uint32_t)(ok && sel_cand(cm, ok ? j : 0)) << i;
+    // (readlane returns a signed int: each half goes through uint32_t so that the low half is not sign-extended)
+    const uint64_t cw = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(mine >> 32), i) << 32) |
+                        (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)mine, i);
+    const bool c = (cw >> lane) & 1ull;  // a mask bit is never set past n
+    raw[i] = typename KeyF::raw_t{};
+    if (cw != 0ull && c) raw[i] = kf.load(row, j0 + 64 * i);  // only the candidates' lanes load
+    valid |= (uint32_t)c << i;
   }
+#pragma unroll
+  for (int i = 0; i < kSelPer; ++i) key[i] = (valid >> i) & 1 ? kf.key(raw[i]) : 0u;
   return valid;
+}
+
+// Adds digit d of every lane with m set to the LDS histogram: the lanes sharing the first active lane's digit add as
+// one atomic, then those sharing the next remaining lane's digit, and the rest one atomic each (a wave's leading bytes
+// mostly fall in one or two bins, where per-lane atomics on one LDS address serialise).
+__device__ __forceinline__ void sel_hist_add(uint32_t* hist, bool m, uint32_t d) {
+  const int lane = threadIdx.x & 63;
+  uint64_t active = __ballot(m);
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    if (active == 0ull) return;
+    const int leader = __ffsll((long long)active) - 1;
+    const uint32_t d0 = __shfl(d, leader, 64);
+    const uint64_t same = __ballot(((active >> lane) & 1ull) && d == d0);
+    if (lane == leader) atomicAdd(&hist[d0], (uint32_t)__popcll(same));
+    active &= ~same;
+  }
+  if ((active >> lane) & 1ull) atomicAdd(&hist[d], 1u);
 }
 
 // Pass `ps` of the histogram of selection `sel` (k of the candidates: every key, or the bits of selection cand_sel).
@@ -381,7 +474,7 @@ __global__ void __launch_bounds__(kSelThreads) sel_hist_kernel(KeyF kf, int n, S
   const int64_t row = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   uint32_t* H = ws.hist + (row * kSelNSel + sel) * 1024;
-  const uint64_t* cm = cand_sel < 0 ? nullptr : ws.mask + (row * kSelNSel + cand_sel) * ws.words;
+  const uint64_t* cm = sel_cmask(ws, row, cand_sel);
   uint32_t prefix, pmask, rem;
   sel_state(H, ps, k, prefix, pmask, rem, sh);
   sh.hist[tid] = 0u;
@@ -395,19 +488,53 @@ __global__ void __launch_bounds__(kSelThreads) sel_hist_kernel(KeyF kf, int n, S
     for (int i = 0; i < kSelPer; ++i) {
       const bool m = ((valid >> i) & 1) && (key[i] & pmask) == prefix;
       const uint32_t d = (key[i] >> shift) & 255u;
-      // lanes whose digit equals the first active lane's add as one (the leading byte is nearly constant per row)
-      const uint64_t active = __ballot(m);
-      if (active) {
-        const int leader = __ffsll((long long)active) - 1;
-        const uint32_t d0 = __shfl(d, leader, 64);
-        const uint64_t same = __ballot(m && d == d0);
-        if (lane == leader) atomicAdd(&sh.hist[d0], (uint32_t)__popcll(same));
-        else if (m && d != d0) atomicAdd(&sh.hist[d], 1u);
-      }
+      sel_hist_add(sh.hist, m, d);
     }
   }
   __syncthreads();
   if (sh.hist[tid] != 0u) atomicAdd(&H[ps * 256 + tid], sh.hist[tid]);
+}
+
+// Step 2 of a selection of k (k >= 1): with the digits of histogram passes 0 and 1 chosen, the 16-bit prefix P of K*.
+// Candidates whose top 16 bits exceed P are taken (their bits are the selection's mask words as written here);
+// candidates whose top 16 bits equal P form the prefix mask, and their bits 15..8 go into histogram pass 2. Every
+// mask word of the chunk is written, in both masks.
+template <class KeyF>
+__global__ void __launch_bounds__(kSelThreads) sel_split_kernel(KeyF kf, int n, SelWs ws, int sel, uint32_t k,
+                                                                 int cand_sel) {
+  __shared__ SelShared sh;
+  const int64_t row = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  uint32_t* H = ws.hist + (row * kSelNSel + sel) * 1024;
+  const uint64_t* cm = sel_cmask(ws, row, cand_sel);
+  uint64_t* out = ws.mask + (row * kSelNSel + sel) * ws.words;
+  uint64_t* pre = ws.pre + row * ws.words;
+  uint32_t prefix, pmask, rem;
+  sel_state(H, 2, k, prefix, pmask, rem, sh);
+  sh.hist[tid] = 0u;
+  __syncthreads();
+  const uint32_t p16 = prefix >> 16;
+  for (int sc = 0; sc < ws.spc; ++sc) {
+    const int js = (blockIdx.x * ws.spc + sc) * kSelChunk + wv * kSelWaveSpan;  // first key of this wave
+    uint32_t key[kSelPer];
+    const uint32_t valid = sel_load(kf, row, js + lane, n, cm, key);
+#pragma unroll
+    for (int i = 0; i < kSelPer; ++i) {
+      const bool v = (valid >> i) & 1;
+      const uint32_t top = key[i] >> 16;
+      const uint64_t am = __ballot(v && top > p16);
+      const bool m = v && top == p16;
+      const uint64_t pm = __ballot(m);
+      const int jw = js + 64 * i;
+      if (lane == 0 && jw < n) {
+        out[jw >> 6] = am;
+        pre[jw >> 6] = pm;
+      }
+      sel_hist_add(sh.hist, m, (key[i] >> 8) & 255u);  // histogram pass 2
+    }
+  }
+  __syncthreads();
+  if (sh.hist[tid] != 0u) atomicAdd(&H[2 * 256 + tid], sh.hist[tid]);
 }
 
 // Candidates equal to K* per chunk.
@@ -417,7 +544,7 @@ __global__ void __launch_bounds__(kSelThreads) sel_eqcount_kernel(KeyF kf, int n
   __shared__ SelShared sh;
   const int64_t row = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const uint64_t* cm = cand_sel < 0 ? nullptr : ws.mask + (row * kSelNSel + cand_sel) * ws.words;
+  const uint64_t* cm = sel_cmask(ws, row, cand_sel);
   uint32_t kstar, pmask, rem;
   sel_state(ws.hist + (row * kSelNSel + sel) * 1024, 4, k, kstar, pmask, rem, sh);
   uint32_t eq = 0;
@@ -450,15 +577,16 @@ __device__ __forceinline__ uint32_t sel_block_sum(const uint32_t* cnt, int m, Se
   return s;
 }
 
-// The selection's bit mask and its population per chunk. k == 0 selects nothing.
+// The selection's bit mask and its population per chunk. k == 0 selects nothing. merge: OR the bits taken here into
+// the mask words already written by sel_split_kernel (the keys above the prefix).
 template <class KeyF>
 __global__ void __launch_bounds__(kSelThreads) sel_mark_kernel(KeyF kf, int n, SelWs ws, int sel, uint32_t k,
-                                                                int cand_sel) {
+                                                                int cand_sel, int merge) {
   __shared__ SelShared sh;
   __shared__ uint32_t weq[kSelThreads / 64];
   const int64_t row = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const uint64_t* cm = cand_sel < 0 ? nullptr : ws.mask + (row * kSelNSel + cand_sel) * ws.words;
+  const uint64_t* cm = sel_cmask(ws, row, cand_sel);
   uint64_t* out = ws.mask + (row * kSelNSel + sel) * ws.words;
   uint32_t kstar = 0, pmask, rem = 0, eq_before = 0;
   if (k > 0) {
@@ -471,6 +599,8 @@ __global__ void __launch_bounds__(kSelThreads) sel_mark_kernel(KeyF kf, int n, S
   uint32_t rank_base = eq_before, taken = 0;
   for (int sc = 0; sc < ws.spc; ++sc) {
     const int js = (blockIdx.x * ws.spc + sc) * kSelChunk + wv * kSelWaveSpan;  // first key of this wave
+    // merge: the wave's kSelPer mask words as sel_split_kernel wrote them, one per lane, read before any is rewritten
+    const uint64_t above = merge && lane < kSelPer && (js >> 6) + lane < ws.words ? out[(js >> 6) + lane] : 0ull;
     uint32_t gtb = 0, eqb = 0, weq_cnt = 0;
     if (k > 0) {
       uint32_t key[kSelPer];
@@ -499,7 +629,9 @@ __global__ void __launch_bounds__(kSelThreads) sel_mark_kernel(KeyF kf, int n, S
         const uint64_t em = __ballot(e);
         const uint32_t my_rank = rank + (uint32_t)__popcll(em & lt);
         const bool take = ((gtb >> i) & 1) || (e && my_rank < rem);
-        const uint64_t tm = __ballot(take);
+        const uint64_t ab = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(above >> 32), i) << 32) |
+                            (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)above, i);
+        const uint64_t tm = __ballot(take) | ab;
         rank += (uint32_t)__popcll(em);
         taken += (uint32_t)__popcll(tm);
         if (lane == 0) out[jw >> 6] = tm;
@@ -553,16 +685,114 @@ __global__ void __launch_bounds__(kSelThreads) sel_emit_kernel(int n, SelWs ws, 
   }
 }
 
-// One selection of k among the candidates (cand_sel's mask, or every key) into mask `sel`.
+// Two-stage top-k, stage 1: the k largest keys of chunk blockIdx.x (kSel2Chunk keys; wave w owns the contiguous
+// kSel2Span keys from w * kSel2Span, lane l the keys l + 64 i), equal keys lowest index first, written as (key, index)
+// in ascending index order to the chunk's k candidate slots. A chunk of fewer than k keys (only the last one) fills
+// its remaining slots with key 0: below every key of the row, and after every other candidate, so never taken
+// (there are at least k real candidates, and among equal keys the lowest slot goes first).
+template <class KeyF>
+__global__ void __launch_bounds__(kTopkThreads) sel2_local_kernel(KeyF kf, int n, int k, SelWs ws) {
+  constexpr int kSel2Span = 64 * kSel2Per;  // keys per wave
+  __shared__ TopkShared sh;
+  __shared__ uint32_t wcnt[kTopkWaves];
+  const int64_t row = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int c0 = blockIdx.x * kSel2Chunk;
+  const int j0 = c0 + wv * kSel2Span + lane;
+  static_assert(sizeof(typename KeyF::raw_t) == 4, "keys formed in place from 32-bit loads");
+  uint32_t key[kSel2Per];  // the loaded bits first, then the keys (in place, so that both fit the register budget)
+#pragma unroll
+  for (int i = 0; i < kSel2Per; ++i)
+    key[i] = j0 + 64 * i < n ? __builtin_bit_cast(uint32_t, kf.load(row, j0 + 64 * i)) : 0u;
+  uint64_t valid = 0;
+#pragma unroll
+  for (int i = 0; i < kSel2Per; ++i) {
+    const bool ok = j0 + 64 * i < n;
+    key[i] = ok ? kf.key(__builtin_bit_cast(typename KeyF::raw_t, key[i])) : 0u;
+    valid |= (uint64_t)ok << i;
+  }
+  const uint32_t kk = (uint32_t)min(k, min(kSel2Chunk, n - c0));  // k <= the chunk's keys except in the last chunk
+  uint32_t kstar, rem;
+  radix_kstar<kSel2Per>(key, valid, kk, sh, kstar, rem);
+  // ranks of the keys equal to K* in index order (wave, step, lane), then the taken keys' slots in the same order
+  const uint64_t lt = (1ull << lane) - 1;
+  uint32_t eqb = 0, weq = 0;
+#pragma unroll
+  for (int i = 0; i < kSel2Per; ++i) {
+    const bool e = ((valid >> i) & 1) && key[i] == kstar;
+    eqb |= (uint32_t)e << i;
+    weq += (uint32_t)__popcll(__ballot(e));
+  }
+  if (lane == 0) wcnt[wv] = weq;
+  __syncthreads();
+  uint32_t rank = 0;
+  for (int w2 = 0; w2 < wv; ++w2) rank += wcnt[w2];
+  __syncthreads();
+  uint32_t takeb = 0, wtake = 0;
+#pragma unroll
+  for (int i = 0; i < kSel2Per; ++i) {
+    const bool e = (eqb >> i) & 1;
+    const uint64_t em = __ballot(e);
+    const bool t = (((valid >> i) & 1) && key[i] > kstar) || (e && rank + (uint32_t)__popcll(em & lt) < rem);
+    rank += (uint32_t)__popcll(em);
+    takeb |= (uint32_t)t << i;
+    wtake += (uint32_t)__popcll(__ballot(t));
+  }
+  if (lane == 0) wcnt[wv] = wtake;
+  __syncthreads();
+  uint32_t pos = 0;
+  for (int w2 = 0; w2 < wv; ++w2) pos += wcnt[w2];
+  const int64_t slot0 = (row * gridDim.x + blockIdx.x) * (int64_t)k;
+  uint32_t* ck = ws.ckey + slot0;
+  int* ci = ws.cidx + slot0;
+#pragma unroll
+  for (int i = 0; i < kSel2Per; ++i) {
+    const bool t = (takeb >> i) & 1;
+    const uint64_t tm = __ballot(t);
+    if (t) {
+      const uint32_t p = pos + (uint32_t)__popcll(tm & lt);
+      ck[p] = key[i];
+      ci[p] = j0 + 64 * i;
+    }
+    pos += (uint32_t)__popcll(tm);
+  }
+  for (int p = (int)kk + tid; p < k; p += kTopkThreads) {
+    ck[p] = 0u;
+    ci[p] = 0;
+  }
+}
+
+// Two-stage top-k, stage 2: the k largest of a row's m = chunks * k candidates (slot order = index order, lowest slot
+// first on equal keys), their indices written in ascending order.
+template <int PER>
+__global__ void __launch_bounds__(kTopkThreads) sel2_merge_kernel(SelWs ws, int m, int k, int64_t* __restrict__ out) {
+  __shared__ TopkShared sh;
+  const uint32_t* kp = ws.ckey + (int64_t)blockIdx.x * m;
+  const int* ip = ws.cidx + (int64_t)blockIdx.x * m;
+  int seg0, cnt;
+  uint64_t all;
+  segment(m, seg0, cnt, all);
+  uint32_t key[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) key[j] = j < cnt ? kp[seg0 + j] : 0u;
+  const uint64_t take = radix_take<PER>(key, all, (uint32_t)k, sh);
+  write_taken_gather(take, seg0, ip, out + (int64_t)blockIdx.x * k, (uint32_t)k, sh);
+}
+
+// One selection of k among the candidates (cand_sel's mask, or every key: kSelAll) into mask `sel`.
 template <class KeyF>
 void sel_run(const KeyF& kf, int rows, int n, const SelWs& ws, int sel, uint32_t k, int cand_sel, hipStream_t st) {
   const dim3 grid(ws.chunks, rows), block(kSelThreads);
-  if (k > 0) {
-    for (int ps = 0; ps < 4; ++ps) hipLaunchKernelGGL(sel_hist_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, ps, k,
-                                                      cand_sel);
-    hipLaunchKernelGGL(sel_eqcount_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, cand_sel);
+  if (k == 0) {
+    hipLaunchKernelGGL(sel_mark_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, cand_sel, 0);
+    return;
   }
-  hipLaunchKernelGGL(sel_mark_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, cand_sel);
+  for (int ps = 0; ps < 2; ++ps)
+    hipLaunchKernelGGL(sel_hist_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, ps, k, cand_sel);
+  hipLaunchKernelGGL(sel_split_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, cand_sel);
+  hipLaunchKernelGGL(sel_hist_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, 3, k, kSelPrefix);
+  hipLaunchKernelGGL(sel_eqcount_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, kSelPrefix);
+  hipLaunchKernelGGL(sel_mark_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, kSelPrefix, 1);
 }
 
 void sel_zero_hist(const SelWs& ws, int rows, hipStream_t st) {
@@ -653,8 +883,22 @@ extern "C" int dgg_topk_select_ws(const float* scores, int64_t rows, int64_t n, 
   SelWs ws;
   if (int rc = sel_check_ws("topk_indices", rows, n, workspace, workspace_bytes, &ws)) return rc;
   hipStream_t st = dgg::as_stream(stream);
+  const KeyScores kf{scores, (int)n, largest ? 1 : 0};
+  const int64_t chunks2 = (n + kSel2Chunk - 1) / kSel2Chunk;
+  if (chunks2 * k <= kSel2MaxCand) {  // two stages: one read of the row
+    const int m = (int)(chunks2 * k);
+    hipLaunchKernelGGL(sel2_local_kernel<KeyScores>, dim3((unsigned)chunks2, (unsigned)rows), dim3(kTopkThreads), 0, st,
+                       kf, (int)n, (int)k, ws);
+    if (m <= 4 * kTopkThreads)
+      hipLaunchKernelGGL(sel2_merge_kernel<4>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, (int)k, out_idx);
+    else if (m <= 16 * kTopkThreads)
+      hipLaunchKernelGGL(sel2_merge_kernel<16>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, (int)k, out_idx);
+    else
+      hipLaunchKernelGGL(sel2_merge_kernel<64>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, (int)k, out_idx);
+    return dgg::check_launch("topk_indices");
+  }
   sel_zero_hist(ws, (int)rows, st);
-  sel_run(KeyScores{scores, (int)n, largest ? 1 : 0}, (int)rows, (int)n, ws, 0, (uint32_t)k, -1, st);
+  sel_run(kf, (int)rows, (int)n, ws, 0, (uint32_t)k, kSelAll, st);
   hipLaunchKernelGGL(sel_emit_kernel, dim3(ws.chunks, (unsigned)rows), dim3(kSelThreads), 0, st, (int)n, ws, 0, -1,
                      out_idx, (int)k);
   return dgg::check_launch("topk_indices");
@@ -681,8 +925,8 @@ extern "C" int dgg_roco_select_ws(const float* score, const float* sq_score, int
   const float rcp = 1.0f / (float)q_len;  // torch's reciprocal of the Python divisor, in fp32
   const int R = (int)rows, N = (int)n;
   sel_zero_hist(ws, R, st);
-  sel_run(KeyStd{score, sq_score, N, rcp, 0}, R, N, ws, 0, (uint32_t)recent, -1, st);      // roco.py:56
-  sel_run(KeyStd{score, sq_score, N, rcp, 1}, R, N, ws, 1, (uint32_t)(n - recent), -1, st);  // roco.py:55
+  sel_run(KeyStd{score, sq_score, N, rcp, 0}, R, N, ws, 0, (uint32_t)recent, kSelAll, st);      // roco.py:56
+  sel_run(KeyStd{score, sq_score, N, rcp, 1}, R, N, ws, 1, (uint32_t)(n - recent), kSelAll, st);  // roco.py:55
   sel_run(KeyMean{score, N, rcp}, R, N, ws, 2, (uint32_t)budget, 1, st);                   // roco.py:57-58
   hipLaunchKernelGGL(sel_emit_kernel, dim3(ws.chunks, (unsigned)rows), dim3(kSelThreads), 0, st, N, ws, 2, 0, out_idx,
                      (int)(budget + recent));

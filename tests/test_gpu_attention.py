@@ -458,6 +458,21 @@ def test_topk_rows_longer_than_65536(gpu, n):
             np.testing.assert_array_equal(got, osel.topk_indices(vals, k, largest), err_msg=f"n={n} k={k} {largest}")
 
 
+@pytest.mark.parametrize("n", [131072, 1048576])
+def test_topk_long_rows_continuous_values(gpu, n):
+    # rows of distinct-looking values (normal, heavy-tailed positive, and a narrow band where the top bits agree):
+    # few keys share the k-th key's 16-bit prefix, so the later passes load only a small part of the row
+    rng = np.random.default_rng(n + 1)
+    vals = np.stack([rng.standard_normal(n), rng.exponential(size=n) ** 3,
+                     1.0 + rng.random(n) * 1e-3]).astype(np.float32)
+    x = torch.from_numpy(vals).to(gpu)
+    for k in (1, 256, 4096, n // 2, n - 1):
+        progress(f"topk continuous n={n} k={k}")
+        for largest in (True, False):
+            got = A.topk_indices(x, k, largest=largest).cpu().numpy()
+            np.testing.assert_array_equal(got, osel.topk_indices(vals, k, largest), err_msg=f"n={n} k={k} {largest}")
+
+
 @pytest.mark.parametrize("n,q_len,recent,budget", [(131072, 4096, 256, 512), (1048576, 100, 4096, 30000),
                                                    (70000, 3, 0, 69999), (70000, 3, 70000, 0)])
 def test_roco_select_rows_longer_than_65536(gpu, n, q_len, recent, budget):

@@ -35,6 +35,13 @@ struct DecodeParams {
   float c;  // scale * log2(e)
 };
 
+// Splits per workgroup: a workgroup runs its splits one after another, writing one partial each, and issues the next
+// split's first loads before it merges the current one. Measured at config 5 (64 splits, 2,048 (b, h), identical
+// outputs): 1 split per workgroup in this loop 5.18-5.27 ms, 2 splits 5.23-5.27, 4 and 8 5.27-5.31, and the earlier
+// for-loop form (loads at the top of each block) 5.27-5.40 ms, in alternating A/Bs on one box. In this loop form the
+// compiler issues the next block's loads into a second register set before the current block's exponentials and
+// P.V accumulation (194 VGPRs); copying V by hand into a second set for the same effect measured no gain.
+constexpr int kSplitsPerWg = 1;
 template <typename T, int D>
 __global__ void __launch_bounds__(kDecThreads) decode_partial_kernel(DecodeParams p) {
   typedef typename T::scalar S;
@@ -45,89 +52,113 @@ __global__ void __launch_bounds__(kDecThreads) decode_partial_kernel(DecodeParam
   __shared__ float sm[GROUPS], sl[GROUPS];
   __shared__ float so[GROUPS][D + 4];
 
-  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int h = blockIdx.y, b = blockIdx.z;
   const int hk = h / p.group;
   const int tid = threadIdx.x;
-  const int grp = tid / LPK;  // 0..GROUPS-1 (row slot inside one workgroup iteration)
+  const int grp = tid / LPK;  // 0..GROUPS-1 (row slot inside one block of key rows)
   const int sub = tid % LPK;  // which 8 head-dim elements
-  const int k0 = split * p.chunk;
-  const int k1 = min(p.L, k0 + p.chunk);
+  const int s_end = min(p.splits, (int)(blockIdx.x + 1) * kSplitsPerWg);
 
   const S* qp = static_cast<const S*>(p.q) + b * p.q_sb + h * p.q_sh;
   const S* kp = static_cast<const S*>(p.k) + b * p.k_sb + hk * p.k_sh + sub * 8;
   const S* vp = static_cast<const S*>(p.v) + b * p.v_sb + hk * p.v_sh + sub * 8;
   f32x8 qv = to_f32x8(ld16<V8>(qp + sub * 8)) * p.c;
 
-  float m = -INFINITY, l = 0.f;
-  f32x8 acc = {};
-  for (int base = k0; base < k1; base += GROUPS * kUnroll) {
-    V8 kr[kUnroll], vr[kUnroll];
-    bool ok[kUnroll];
+  V8 kr[kUnroll], vr[kUnroll];
+  bool ok[kUnroll];
+  // Loads of the block of GROUPS * kUnroll key rows from `base` of a split ending at k1 > base. Keys past the end
+  // re-read its last key (finite; masked to p = 0 below), so that all 2*kUnroll loads go out back to back: a load
+  // under a per-lane branch is waited for on its own. Non-temporal: each cache row is read once (5.55 -> 5.33 ms at
+  // config 5).
+  auto issue = [&](int base, int k1) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      // Keys past the split's end re-read its last key (finite; masked to p = 0 below), so that all 2*kUnroll
-      // loads go out back to back: a load under a per-lane branch is waited for on its own.
       const int key = base + u * GROUPS + grp;
       ok[u] = key < k1;
       const int kc = min(key, k1 - 1);
-      // non-temporal: each cache row is read once (5.55 -> 5.33 ms at config 5)
       kr[u] = __builtin_nontemporal_load(reinterpret_cast<const V8*>(kp + (int64_t)kc * p.k_sl));
       vr[u] = __builtin_nontemporal_load(reinterpret_cast<const V8*>(vp + (int64_t)kc * p.v_sl));
     }
-    float s[kUnroll];
-    float bm = -INFINITY;
+  };
+  int split = blockIdx.x * kSplitsPerWg;
+  int k1 = min(p.L, split * p.chunk + p.chunk);
+  int base = split * p.chunk;
+  if (base < k1) issue(base, k1);
+  float m = -INFINITY, l = 0.f;
+  f32x8 acc = {};
+  while (true) {
+    if (base < k1) {
+      float s[kUnroll];
+      float bm = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const f32x8 kf = to_f32x8(kr[u]);
-      float d = 0.f;
+      for (int u = 0; u < kUnroll; ++u) {
+        const f32x8 kf = to_f32x8(kr[u]);
+        float d = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) d = fmaf(qv[e], kf[e], d);
+        for (int e = 0; e < 8; ++e) d = fmaf(qv[e], kf[e], d);
 #pragma unroll
-      for (int off = LPK / 2; off >= 1; off >>= 1) d += __shfl_xor(d, off, 64);
-      s[u] = ok[u] ? d : -INFINITY;
-      bm = fmaxf(bm, s[u]);
+        for (int off = LPK / 2; off >= 1; off >>= 1) d += __shfl_xor(d, off, 64);
+        s[u] = ok[u] ? d : -INFINITY;
+        bm = fmaxf(bm, s[u]);
+      }
+      const float m_new = fmaxf(m, bm);
+      if (m_new > m) {
+        const float alpha = fast_exp2(m - m_new);  // m == -inf -> 0
+        l *= alpha;
+        acc *= alpha;
+        m = m_new;
+      }
+      const float mu = m == -INFINITY ? 0.f : m;
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const float pe = fast_exp2(s[u] - mu);
+        l += pe;
+        acc += pe * to_f32x8(vr[u]);
+      }
+      base += GROUPS * kUnroll;
+      if (base < k1) {
+        issue(base, k1);
+        continue;
+      }
     }
-    const float m_new = fmaxf(m, bm);
-    if (m_new > m) {
-      const float alpha = fast_exp2(m - m_new);  // m == -inf -> 0
-      l *= alpha;
-      acc *= alpha;
-      m = m_new;
+    // The split is done: the next split's first loads go out, then the lane groups' states of this split are merged
+    // through LDS into its partial (unnormalised output, max, sum).
+    const int nsplit = split + 1;
+    const int nbase = nsplit * p.chunk, nk1 = min(p.L, nbase + p.chunk);
+    if (nsplit < s_end && nbase < nk1) issue(nbase, nk1);
+    if (sub == 0) {
+      sm[grp] = m;
+      sl[grp] = l;
     }
-    const float mu = m == -INFINITY ? 0.f : m;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const float pe = fast_exp2(s[u] - mu);
-      l += pe;
-      acc += pe * to_f32x8(vr[u]);
+    for (int e = 0; e < 8; ++e) so[grp][sub * 8 + e] = acc[e];
+    __syncthreads();
+    float M = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < GROUPS; ++i) M = fmaxf(M, sm[i]);
+    const float Mu = M == -INFINITY ? 0.f : M;
+    const int64_t pidx = ((int64_t)b * p.Hq + h) * p.splits + split;
+    for (int d = tid; d < D; d += kDecThreads) {
+      float od = 0.f;
+#pragma unroll
+      for (int i = 0; i < GROUPS; ++i) od += fast_exp2(sm[i] - Mu) * so[i][d];
+      p.part_o[pidx * D + d] = od;
     }
-  }
-
-  // Merge the lane groups of the workgroup through LDS.
-  if (sub == 0) {
-    sm[grp] = m;
-    sl[grp] = l;
-  }
+    if (tid == 0) {
+      float L = 0.f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) so[grp][sub * 8 + e] = acc[e];
-  __syncthreads();
-  float M = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < GROUPS; ++i) M = fmaxf(M, sm[i]);
-  const float Mu = M == -INFINITY ? 0.f : M;
-  const int64_t pidx = ((int64_t)b * p.Hq + h) * p.splits + split;
-  for (int d = tid; d < D; d += kDecThreads) {
-    float od = 0.f;
-#pragma unroll
-    for (int i = 0; i < GROUPS; ++i) od += fast_exp2(sm[i] - Mu) * so[i][d];
-    p.part_o[pidx * D + d] = od;
-  }
-  if (tid == 0) {
-    float L = 0.f;
-#pragma unroll
-    for (int i = 0; i < GROUPS; ++i) L += fast_exp2(sm[i] - Mu) * sl[i];
-    p.part_ml[pidx * 2 + 0] = M;
-    p.part_ml[pidx * 2 + 1] = L;
+      for (int i = 0; i < GROUPS; ++i) L += fast_exp2(sm[i] - Mu) * sl[i];
+      p.part_ml[pidx * 2 + 0] = M;
+      p.part_ml[pidx * 2 + 1] = L;
+    }
+    if (nsplit >= s_end) break;
+    __syncthreads();  // every lane group has read sm / sl / so before the next split's merge rewrites them
+    split = nsplit;
+    base = nbase;
+    k1 = nk1;
+    m = -INFINITY;
+    l = 0.f;
+    acc = f32x8{};
   }
 }
 
@@ -160,7 +191,7 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams p) {
 
 template <typename T, int D>
 void launch_decode(const DecodeParams& p, hipStream_t st) {
-  hipLaunchKernelGGL((decode_partial_kernel<T, D>), dim3(p.splits, p.Hq, p.B), dim3(kDecThreads), 0, st, p);
+  hipLaunchKernelGGL((decode_partial_kernel<T, D>), dim3((p.splits + kSplitsPerWg - 1) / kSplitsPerWg, p.Hq, p.B), dim3(kDecThreads), 0, st, p);
   hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(p.Hq, p.B), dim3(D < 256 ? 128 : 256), 0, st, p);
 }
 

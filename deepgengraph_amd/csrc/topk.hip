@@ -288,8 +288,8 @@ struct SelWs {
   uint32_t* mcnt;   // [rows][kSelNSel][chunks]
   uint64_t* mask;   // [rows][kSelNSel][words]
   uint64_t* pre;    // [rows][words]: the prefix mask of the selection in progress
-  uint32_t* ckey;   // [rows][kSel2MaxCand]: two-stage candidates (top-k with chunks * k <= kSel2MaxCand)
-  int* cidx;        // [rows][kSel2MaxCand]
+  uint32_t* ckey;   // two-stage candidates, [rows][m] with m = chunks * k <= kSel2MaxCand (room for kSel2MaxCand per row)
+  int* cidx;        // their indices, same layout
   int chunks, words;
   int spc;          // kSelChunk-key sub-chunks per workgroup (a chunk is spc * kSelChunk keys)
 };

@@ -1523,6 +1523,11 @@ void launch_colsum(const AttnParams& p, hipStream_t st) {
 #ifndef DGG_D128_BN
 #define DGG_D128_BN 128
 #endif
+// DGG_D128_OCC: waves per SIMD the register budget is sized for (2; 3 with DGG_D128_NW=4 DGG_D128_BN=32 is the
+// three-waves-per-SIMD form, whose LDS fits three workgroups per CU only at 32-key tiles).
+#ifndef DGG_D128_OCC
+#define DGG_D128_OCC 2
+#endif
 constexpr int kD128NQB = 1, kD128NW = DGG_D128_NW, kD128BN = DGG_D128_BN, kD128NS = 2;
 constexpr int kD128BM = 32 * kD128NQB * kD128NW;  // query rows per workgroup (head_dim 128)
 
@@ -1531,11 +1536,11 @@ void launch_fwd_d128(const AttnParams& p, hipStream_t st) {
   const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
   if (!REFROUND && p.lse == nullptr)
     hipLaunchKernelGGL(
-        (attn_fwd_dma_kernel<T, 128, kD128NQB, kD128NW, kD128BN, kD128NS, 2, MASK, SOFTCAP, REFROUND, !REFROUND>),
+        (attn_fwd_dma_kernel<T, 128, kD128NQB, kD128NW, kD128BN, kD128NS, DGG_D128_OCC, MASK, SOFTCAP, REFROUND, !REFROUND>),
         dim3(grid), dim3(64 * kD128NW), 0, st, p);
   else
     hipLaunchKernelGGL(
-        (attn_fwd_dma_kernel<T, 128, kD128NQB, kD128NW, kD128BN, kD128NS, 2, MASK, SOFTCAP, REFROUND, false>),
+        (attn_fwd_dma_kernel<T, 128, kD128NQB, kD128NW, kD128BN, kD128NS, DGG_D128_OCC, MASK, SOFTCAP, REFROUND, false>),
         dim3(grid), dim3(64 * kD128NW), 0, st, p);
 }
 

@@ -72,9 +72,24 @@ def splitkv_splits(B: int, Sq: int, Hq: int, Hkv: int, span: int) -> int:
 
 
 def decode_splits(B: int, Hq: int, L: int) -> int:
-    """Split count for a decode call: at least ~2048 workgroups over the chip (8 per CU) when the cache allows,
-    and at least 128 keys per split (one unrolled block of the partial kernel)."""
-    want = -(-2048 // max(1, B * Hq))
+    """Split count for a decode call: enough splits for ~512 workgroups, and up to 8 splits of at least 4,096 keys
+    (a split costs a partial and its share of the merge, so beyond that more of them only adds work), with at least
+    128 keys per split (one unrolled block of the partial kernel). Measured on MI355X, fp16, D=128, us per call:
+
+    ============================  ==============================================  ======
+    shape (B, H, L)               splits: time                                    picked
+    ============================  ==============================================  ======
+    64, 32, 32768 [B, L, H, D]    1: 5,280-5,310  2: 5,121  8: 4,939  32: 5,314      8
+    64, 32, 32768 [B, H, L, D]    1: 4,880  8: 4,877  32: 5,019 (flat)               8
+    1, 32, 32768                  4: 128  8: 90  16: 86  64: 96  256: 148           16
+    4, 32, 32768                  2: 323  8: 318  16: 320  64: 336                   8
+    1, 32, 4096                   2: 36  8: 19  16: 18  32: 23                      16
+    8, 8, 131072                  2: 891  4: 612  8: 618  64: 634                    8
+    16, 32, 8192                  2: 316  4: 315  16: 328  64: 362                   2
+    2, 8, 65536                   4: 230  16: 93  32: 90  64: 96                    32
+    ============================  ==============================================  ======
+    """
+    want = max(-(-512 // max(1, B * Hq)), min(8, -(-L // 4096)))
     return int(max(1, min(1024, want, -(-L // 128))))
 
 

@@ -473,6 +473,23 @@ def test_topk_long_rows_continuous_values(gpu, n):
             np.testing.assert_array_equal(got, osel.topk_indices(vals, k, largest), err_msg=f"n={n} k={k} {largest}")
 
 
+def test_topk_long_rows_two_stage_boundary(gpu):
+    # at 1,048,576 keys (64 chunks of 16,384) k = 1,024 is the largest k of the two-stage selection (64 x 1,024
+    # candidates, the merge's 64-per-thread form) and k = 1,025 the smallest of the pass form; ties across chunk
+    # borders (a value repeated every 1,000 keys) decide both
+    n = 1048576
+    rng = np.random.default_rng(11)
+    vals = rng.standard_normal((2, n)).astype(np.float32)
+    vals[0, ::1000] = 3.5
+    vals[1] = np.round(vals[1] * 4) / 4
+    x = torch.from_numpy(vals).to(gpu)
+    for k in (1024, 1025):
+        progress(f"topk two-stage boundary n={n} k={k}")
+        for largest in (True, False):
+            got = A.topk_indices(x, k, largest=largest).cpu().numpy()
+            np.testing.assert_array_equal(got, osel.topk_indices(vals, k, largest), err_msg=f"n={n} k={k} {largest}")
+
+
 @pytest.mark.parametrize("n,q_len,recent,budget", [(131072, 4096, 256, 512), (1048576, 100, 4096, 30000),
                                                    (70000, 3, 0, 69999), (70000, 3, 70000, 0)])
 def test_roco_select_rows_longer_than_65536(gpu, n, q_len, recent, budget):

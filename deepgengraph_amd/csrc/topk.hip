@@ -685,13 +685,15 @@ __global__ void __launch_bounds__(kSelThreads) sel_emit_kernel(int n, SelWs ws, 
   }
 }
 
-// Two-stage top-k, stage 1: the k largest keys of chunk blockIdx.x (kSel2Chunk keys; wave w owns the contiguous
-// kSel2Span keys from w * kSel2Span, lane l the keys l + 64 i), equal keys lowest index first, written as (key, index)
-// in ascending index order to the chunk's k candidate slots. A chunk of fewer than k keys (only the last one) fills
-// its remaining slots with key 0: below every key of the row, and after every other candidate, so never taken
-// (there are at least k real candidates, and among equal keys the lowest slot goes first).
+// Two-stage top-k, stage 1: the k largest candidate keys of chunk blockIdx.x (kSel2Chunk keys; wave w owns the
+// contiguous kSel2Span keys from w * kSel2Span, lane l the keys l + 64 i; the candidates are every key, or the bits
+// of an earlier selection's mask), equal keys lowest index first, written as (key, index) in ascending index order to
+// the chunk's k candidate slots. A chunk of fewer than k candidates fills its remaining slots with key 0, which is
+// never taken: the row holds at least k candidates, and every key is above 0 (order keys of the largest-first
+// direction; NaN maps to the top) or, for KeyScores' smallest-first keys, where NaN maps to 0, without a mask only
+// the last chunk pads, after every other slot, and among equal keys the lowest slot goes first.
 template <class KeyF>
-__global__ void __launch_bounds__(kTopkThreads) sel2_local_kernel(KeyF kf, int n, int k, SelWs ws) {
+__global__ void __launch_bounds__(kTopkThreads) sel2_local_kernel(KeyF kf, int n, int k, SelWs ws, int cand_sel) {
   constexpr int kSel2Span = 64 * kSel2Per;  // keys per wave
   __shared__ TopkShared sh;
   __shared__ uint32_t wcnt[kTopkWaves];
@@ -699,19 +701,58 @@ __global__ void __launch_bounds__(kTopkThreads) sel2_local_kernel(KeyF kf, int n
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int c0 = blockIdx.x * kSel2Chunk;
   const int j0 = c0 + wv * kSel2Span + lane;
-  static_assert(sizeof(typename KeyF::raw_t) == 4, "keys formed in place from 32-bit loads");
-  uint32_t key[kSel2Per];  // the loaded bits first, then the keys (in place, so that both fit the register budget)
-#pragma unroll
-  for (int i = 0; i < kSel2Per; ++i)
-    key[i] = j0 + 64 * i < n ? __builtin_bit_cast(uint32_t, kf.load(row, j0 + 64 * i)) : 0u;
+  uint32_t key[kSel2Per];
   uint64_t valid = 0;
+  const uint64_t* cm = sel_cmask(ws, row, cand_sel);
+  if constexpr (sizeof(typename KeyF::raw_t) == 4) {
+    // the loaded bits first, then the keys (in place, so that both fit the register budget)
 #pragma unroll
-  for (int i = 0; i < kSel2Per; ++i) {
-    const bool ok = j0 + 64 * i < n;
-    key[i] = ok ? kf.key(__builtin_bit_cast(typename KeyF::raw_t, key[i])) : 0u;
-    valid |= (uint64_t)ok << i;
+    for (int i = 0; i < kSel2Per; ++i)
+      key[i] = j0 + 64 * i < n ? __builtin_bit_cast(uint32_t, kf.load(row, j0 + 64 * i)) : 0u;
+#pragma unroll
+    for (int i = 0; i < kSel2Per; ++i) {
+      const bool ok = j0 + 64 * i < n;
+      key[i] = ok ? kf.key(__builtin_bit_cast(typename KeyF::raw_t, key[i])) : 0u;
+      valid |= (uint64_t)ok << i;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kSel2Per; ++i) {
+      const bool ok = j0 + 64 * i < n;
+      key[i] = ok ? kf.key(kf.load(row, j0 + 64 * i)) : 0u;
+      valid |= (uint64_t)ok << i;
+    }
   }
-  const uint32_t kk = (uint32_t)min(k, min(kSel2Chunk, n - c0));  // k <= the chunk's keys except in the last chunk
+  uint32_t cnt_chunk = (uint32_t)min(kSel2Chunk, n - c0);
+  if (cm != nullptr) {  // candidates: the mask's bits (step i covers mask word (j0 - lane) / 64 + i)
+    const int w0 = (j0 - lane) >> 6, nwords = (n + 63) >> 6;
+    const uint64_t mine = lane < kSel2Per && w0 + lane < nwords ? cm[w0 + lane] : 0ull;
+    uint32_t vmask = 0;
+#pragma unroll
+    for (int i = 0; i < kSel2Per; ++i) {
+      const uint64_t cw = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(mine >> 32), i) << 32) |
+                          (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)mine, i);
+      vmask |= (uint32_t)((cw >> lane) & 1ull) << i;
+    }
+    valid &= vmask;
+    uint32_t c = __popc((uint32_t)valid);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off, 64);
+    if (lane == 0) wcnt[wv] = c;
+    __syncthreads();
+    cnt_chunk = 0;
+    for (int w2 = 0; w2 < kTopkWaves; ++w2) cnt_chunk += wcnt[w2];
+    __syncthreads();
+  }
+  const uint32_t kk = min((uint32_t)k, cnt_chunk);  // k <= the chunk's candidates, or all of them
+  const int64_t slot0 = (row * gridDim.x + blockIdx.x) * (int64_t)k;
+  uint32_t* ck = ws.ckey + slot0;
+  int* ci = ws.cidx + slot0;
+  for (int q = (int)kk + tid; q < k; q += kTopkThreads) {
+    ck[q] = 0u;
+    ci[q] = 0;
+  }
+  if (kk == 0) return;  // (uniform over the workgroup)
   uint32_t kstar, rem;
   radix_kstar<kSel2Per>(key, valid, kk, sh, kstar, rem);
   // ranks of the keys equal to K* in index order (wave, step, lane), then the taken keys' slots in the same order
@@ -742,9 +783,6 @@ __global__ void __launch_bounds__(kTopkThreads) sel2_local_kernel(KeyF kf, int n
   __syncthreads();
   uint32_t pos = 0;
   for (int w2 = 0; w2 < wv; ++w2) pos += wcnt[w2];
-  const int64_t slot0 = (row * gridDim.x + blockIdx.x) * (int64_t)k;
-  uint32_t* ck = ws.ckey + slot0;
-  int* ci = ws.cidx + slot0;
 #pragma unroll
   for (int i = 0; i < kSel2Per; ++i) {
     const bool t = (takeb >> i) & 1;
@@ -756,16 +794,13 @@ __global__ void __launch_bounds__(kTopkThreads) sel2_local_kernel(KeyF kf, int n
     }
     pos += (uint32_t)__popcll(tm);
   }
-  for (int p = (int)kk + tid; p < k; p += kTopkThreads) {
-    ck[p] = 0u;
-    ci[p] = 0;
-  }
 }
 
 // Two-stage top-k, stage 2: the k largest of a row's m = chunks * k candidates (slot order = index order, lowest slot
 // first on equal keys), their indices written in ascending order.
 template <int PER>
-__global__ void __launch_bounds__(kTopkThreads) sel2_merge_kernel(SelWs ws, int m, int k, int64_t* __restrict__ out) {
+__global__ void __launch_bounds__(kTopkThreads) sel2_merge_kernel(SelWs ws, int m, int k, int64_t* __restrict__ out,
+                                                                   int64_t out_rs) {
   __shared__ TopkShared sh;
   const uint32_t* kp = ws.ckey + (int64_t)blockIdx.x * m;
   const int* ip = ws.cidx + (int64_t)blockIdx.x * m;
@@ -776,7 +811,54 @@ __global__ void __launch_bounds__(kTopkThreads) sel2_merge_kernel(SelWs ws, int 
 #pragma unroll
   for (int j = 0; j < PER; ++j) key[j] = j < cnt ? kp[seg0 + j] : 0u;
   const uint64_t take = radix_take<PER>(key, all, (uint32_t)k, sh);
-  write_taken_gather(take, seg0, ip, out + (int64_t)blockIdx.x * k, (uint32_t)k, sh);
+  write_taken_gather(take, seg0, ip, out + (int64_t)blockIdx.x * out_rs, (uint32_t)k, sh);
+}
+
+// Both stages of a two-stage selection of k (chunks * k <= kSel2MaxCand) into out [rows] with row stride out_rs.
+template <class KeyF>
+void sel2_run(const KeyF& kf, int rows, int n, int k, const SelWs& ws, int cand_sel, int64_t* out, int64_t out_rs,
+              hipStream_t st) {
+  const int chunks = (n + kSel2Chunk - 1) / kSel2Chunk, m = chunks * k;
+  hipLaunchKernelGGL(sel2_local_kernel<KeyF>, dim3((unsigned)chunks, (unsigned)rows), dim3(kTopkThreads), 0, st, kf, n,
+                     k, ws, cand_sel);
+  if (m <= 4 * kTopkThreads)
+    hipLaunchKernelGGL(sel2_merge_kernel<4>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, k, out, out_rs);
+  else if (m <= 16 * kTopkThreads)
+    hipLaunchKernelGGL(sel2_merge_kernel<16>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, k, out, out_rs);
+  else
+    hipLaunchKernelGGL(sel2_merge_kernel<64>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, k, out, out_rs);
+}
+
+// RoCo's output from its two two-stage selections: row r of out holds pick's `na` indices then recent's `nb`, each
+// ascending; they are merged in place into one ascending list (an index in both written twice). One workgroup per
+// row; both lists go through LDS as 32-bit indices (n <= 2^26), na + nb <= kRocoMergeMax.
+constexpr int kRocoMergeMax = 16384;
+__global__ void __launch_bounds__(256) roco_merge_kernel(int64_t* __restrict__ out, int na, int nb) {
+  __shared__ int la[kRocoMergeMax];
+  int* lb = la + na;
+  int64_t* o = out + (int64_t)blockIdx.x * (na + nb);
+  for (int i = threadIdx.x; i < na + nb; i += 256) la[i] = (int)o[i];
+  __syncthreads();
+  for (int i = threadIdx.x; i < na; i += 256) {  // position: i + the recent indices below it
+    const int x = la[i];
+    int lo = 0, hi = nb;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (lb[mid] < x) lo = mid + 1;
+      else hi = mid;
+    }
+    o[i + lo] = x;
+  }
+  for (int j = threadIdx.x; j < nb; j += 256) {  // position: j + the pick indices at or below it
+    const int x = lb[j];
+    int lo = 0, hi = na;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (la[mid] <= x) lo = mid + 1;
+      else hi = mid;
+    }
+    o[j + lo] = x;
+  }
 }
 
 // One selection of k among the candidates (cand_sel's mask, or every key: kSelAll) into mask `sel`.
@@ -886,15 +968,7 @@ extern "C" int dgg_topk_select_ws(const float* scores, int64_t rows, int64_t n, 
   const KeyScores kf{scores, (int)n, largest ? 1 : 0};
   const int64_t chunks2 = (n + kSel2Chunk - 1) / kSel2Chunk;
   if (chunks2 * k <= kSel2MaxCand) {  // two stages: one read of the row
-    const int m = (int)(chunks2 * k);
-    hipLaunchKernelGGL(sel2_local_kernel<KeyScores>, dim3((unsigned)chunks2, (unsigned)rows), dim3(kTopkThreads), 0, st,
-                       kf, (int)n, (int)k, ws);
-    if (m <= 4 * kTopkThreads)
-      hipLaunchKernelGGL(sel2_merge_kernel<4>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, (int)k, out_idx);
-    else if (m <= 16 * kTopkThreads)
-      hipLaunchKernelGGL(sel2_merge_kernel<16>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, (int)k, out_idx);
-    else
-      hipLaunchKernelGGL(sel2_merge_kernel<64>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, (int)k, out_idx);
+    sel2_run(kf, (int)rows, (int)n, (int)k, ws, kSelAll, out_idx, k, st);
     return dgg::check_launch("topk_indices");
   }
   sel_zero_hist(ws, (int)rows, st);
@@ -924,6 +998,21 @@ extern "C" int dgg_roco_select_ws(const float* score, const float* sq_score, int
   hipStream_t st = dgg::as_stream(stream);
   const float rcp = 1.0f / (float)q_len;  // torch's reciprocal of the Python divisor, in fp32
   const int R = (int)rows, N = (int)n;
+  const int64_t chunks2 = (n + kSel2Chunk - 1) / kSel2Chunk;
+  if (chunks2 * std::max(recent, budget) <= kSel2MaxCand && budget + recent <= kRocoMergeMax) {
+    // recent and pick in two stages (pick among other's mask), other in passes; the two index lists are written to
+    // out's rows (pick first) and merged in place
+    const int64_t rs = budget + recent;
+    sel_zero_hist(ws, R, st);
+    if (recent > 0) sel2_run(KeyStd{score, sq_score, N, rcp, 0}, R, N, (int)recent, ws, kSelAll, out_idx + budget, rs, st);
+    if (budget > 0) {
+      sel_run(KeyStd{score, sq_score, N, rcp, 1}, R, N, ws, 1, (uint32_t)(n - recent), kSelAll, st);  // roco.py:55
+      sel2_run(KeyMean{score, N, rcp}, R, N, (int)budget, ws, 1, out_idx, rs, st);                  // roco.py:57-58
+    }
+    if (budget > 0 && recent > 0)
+      hipLaunchKernelGGL(roco_merge_kernel, dim3((unsigned)rows), dim3(256), 0, st, out_idx, (int)budget, (int)recent);
+    return dgg::check_launch("roco_select");
+  }
   sel_zero_hist(ws, R, st);
   sel_run(KeyStd{score, sq_score, N, rcp, 0}, R, N, ws, 0, (uint32_t)recent, kSelAll, st);      // roco.py:56
   sel_run(KeyStd{score, sq_score, N, rcp, 1}, R, N, ws, 1, (uint32_t)(n - recent), kSelAll, st);  // roco.py:55

@@ -491,9 +491,12 @@ def test_topk_long_rows_two_stage_boundary(gpu):
 
 
 @pytest.mark.parametrize("n,q_len,recent,budget", [(131072, 4096, 256, 512), (1048576, 100, 4096, 30000),
-                                                   (70000, 3, 0, 69999), (70000, 3, 70000, 0)])
+                                                   (70000, 3, 0, 69999), (70000, 3, 70000, 0),
+                                                   (131072, 4096, 0, 700), (131072, 4096, 700, 0),
+                                                   (200000, 50, 1000, 3000)])
 def test_roco_select_rows_longer_than_65536(gpu, n, q_len, recent, budget):
-    # RoCo's three chained selections over several workgroups per row, with ties and NaN std (negative variance)
+    # RoCo's three chained selections over several workgroups per row, with ties and NaN std (negative variance);
+    # recent and pick in two stages where chunks * k allows (the first, last three cases), else all in passes
     rng = np.random.default_rng(n + recent)
     s1 = rng.integers(0, 50, size=(2, n)).astype(np.float32)
     s2 = rng.integers(0, 80, size=(2, n)).astype(np.float32) / 2.0

@@ -246,9 +246,11 @@ __global__ void __launch_bounds__(kTopkThreads) roco_select_kernel(const float* 
 
 // ------------------------------------------------------------------------------------------------
 // Rows longer than 65536 keys: the same selections (same key order, same tie rule, same output order) over many
-// workgroups per row, in passes through a caller-provided workspace. A row is cut into chunks of kSelChunk keys, one
-// 256-thread workgroup per (chunk, row); wave w of a chunk owns its contiguous kSelWaveSpan keys, 64 at a time
-// (lane l on key 64i + l), so a 64-bit ballot is one aligned word of a bit mask.
+// workgroups per row, through a caller-provided workspace, in one of two forms. A selection of k with
+// ceil(n / kSel2Chunk) * k <= kSel2MaxCand runs in two stages (sel2_local_kernel, sel2_merge_kernel): each chunk's k
+// largest as candidates, then k among those, reading the row once. Other selections run in passes: a row is cut into
+// chunks of kSelChunk keys, one 256-thread workgroup per (chunk, row); wave w of a chunk owns its contiguous
+// kSelWaveSpan keys, 64 at a time (lane l on key 64i + l), so a 64-bit ballot is one aligned word of a bit mask.
 //   1. two histogram passes: pass p counts the candidates whose key matches the digits chosen so far into 256 bins
 //      of its byte (LDS, then one global atomic per bin and workgroup); every workgroup of the next pass re-derives
 //      the chosen digits from the finished histograms (a 256-bin suffix scan per pass);
@@ -267,7 +269,9 @@ __global__ void __launch_bounds__(kTopkThreads) roco_select_kernel(const float* 
 // Steps 1 and 2 read every key (three reads of the row); steps 3-5 load only the keys of mask words that hold a
 // prefix-mask bit, which for scores in general is a small share of the row (all of it when every key is equal).
 // RoCo chains three selections: `recent` (largest std), `other` (smallest std), `pick` (largest mean among the
-// candidates of `other`'s mask), then writes pick and recent.
+// candidates of `other`'s mask), then writes pick and recent merged. `recent` and `pick` take the two-stage form when
+// both fit it (their sorted lists then go to the output rows and roco_merge_kernel merges them); `other`, whose k is
+// n - recent, runs in passes.
 // ------------------------------------------------------------------------------------------------
 constexpr int kSelThreads = 256;
 constexpr int kSelPer = 16;                                 // keys per lane per chunk, loaded back to back

@@ -493,10 +493,13 @@ def test_topk_long_rows_two_stage_boundary(gpu):
 @pytest.mark.parametrize("n,q_len,recent,budget", [(131072, 4096, 256, 512), (1048576, 100, 4096, 30000),
                                                    (70000, 3, 0, 69999), (70000, 3, 70000, 0),
                                                    (131072, 4096, 0, 700), (131072, 4096, 700, 0),
-                                                   (200000, 50, 1000, 3000)])
+                                                   (200000, 50, 1000, 3000),
+                                                   (65600, 7, 3277, 13107), (65600, 7, 3278, 13107)])
 def test_roco_select_rows_longer_than_65536(gpu, n, q_len, recent, budget):
     # RoCo's three chained selections over several workgroups per row, with ties and NaN std (negative variance);
-    # recent and pick in two stages where chunks * k allows (the first, last three cases), else all in passes
+    # recent and pick in two stages where chunks * k allows (the first and the fifth to eighth cases), else all in
+    # passes. The last two sit at the in-place merge's limit of 16,384 indices per row (5 chunks x 13,107 candidates
+    # fits the two-stage form): exactly at it, then one index past it (all in passes)
     rng = np.random.default_rng(n + recent)
     s1 = rng.integers(0, 50, size=(2, n)).astype(np.float32)
     s2 = rng.integers(0, 80, size=(2, n)).astype(np.float32) / 2.0

@@ -82,6 +82,7 @@ def _variant(fn, iters: int, warm_ms: float = 60.0):
     (ms, info) with the warm-up call count and the shader clock just before and after the timed calls."""
     dev = torch.cuda.current_device()
     clk = torch.zeros(2, 2, dtype=torch.int64, device=dev)
+    fn()  # the first call carries one-time host work (allocations, lazy set-up); the second sizes the warm-up
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     fn()
@@ -94,7 +95,7 @@ def _variant(fn, iters: int, warm_ms: float = 60.0):
     ms = _events_time(fn, iters, 0)
     _clock_probe(dev, clk, 1)
     torch.cuda.synchronize()
-    return ms, dict(warmup=warm + 1, clock_mhz=[_clock_mhz(clk, 0), _clock_mhz(clk, 1)])
+    return ms, dict(warmup=warm + 2, clock_mhz=[_clock_mhz(clk, 0), _clock_mhz(clk, 1)])
 
 
 def _clock_probe(dev, buf, slot):

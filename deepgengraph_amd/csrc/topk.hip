@@ -127,10 +127,15 @@ __device__ void radix_kstar(const uint32_t (&key)[PER], uint64_t cand, uint32_t 
 }
 
 template <int PER>
-__device__ uint64_t radix_take(const uint32_t (&key)[PER], uint64_t cand, uint32_t k, TopkShared& sh) {
+__device__ uint64_t radix_take(const uint32_t (&key)[PER], uint64_t cand, uint32_t k, TopkShared& sh,
+                               uint32_t* bound = nullptr) {
   if (k == 0) return 0;
   uint32_t prefix, remaining;
   radix_kstar<PER>(key, cand, k, sh, prefix, remaining);
+  if (bound != nullptr && threadIdx.x == 0) {  // K* and how many keys equal to it are taken
+    bound[0] = prefix;
+    bound[1] = remaining;
+  }
   // prefix = K*; `remaining` candidates equal to K* are still to be taken, lowest index first.
   uint32_t eq = 0;
 #pragma unroll
@@ -409,6 +414,9 @@ __device__ __forceinline__ const uint64_t* sel_cmask(const SelWs& ws, int64_t ro
   if (cand == kSelPrefix) return ws.pre + row * ws.words;
   return cand < 0 ? nullptr : ws.mask + (row * kSelNSel + cand) * ws.words;
 }
+// A two-stage selection's boundary of row `row`, {K*, keys equal to K* taken}, kept in the first two words of the row's
+// selection-0 histogram (which a two-stage selection does not use).
+__device__ __forceinline__ uint32_t* sel_bound(const SelWs& ws, int64_t row) { return ws.hist + row * kSelNSel * 1024; }
 
 __global__ void __launch_bounds__(256) sel_zero_kernel(uint32_t* p, int64_t count) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) p[i] = 0u;
@@ -541,16 +549,18 @@ __global__ void __launch_bounds__(kSelThreads) sel_split_kernel(KeyF kf, int n, 
   if (sh.hist[tid] != 0u) atomicAdd(&H[2 * 256 + tid], sh.hist[tid]);
 }
 
-// Candidates equal to K* per chunk.
+// Candidates equal to K* per chunk. comp: K* is the complement of the K* of the two-stage selection whose boundary
+// sel_bound holds (see sel_mark_kernel).
 template <class KeyF>
 __global__ void __launch_bounds__(kSelThreads) sel_eqcount_kernel(KeyF kf, int n, SelWs ws, int sel, uint32_t k,
-                                                                   int cand_sel) {
+                                                                   int cand_sel, int comp) {
   __shared__ SelShared sh;
   const int64_t row = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint64_t* cm = sel_cmask(ws, row, cand_sel);
   uint32_t kstar, pmask, rem;
-  sel_state(ws.hist + (row * kSelNSel + sel) * 1024, 4, k, kstar, pmask, rem, sh);
+  if (comp) kstar = ~sel_bound(ws, row)[0];
+  else sel_state(ws.hist + (row * kSelNSel + sel) * 1024, 4, k, kstar, pmask, rem, sh);
   uint32_t eq = 0;
   for (int sc = 0; sc < ws.spc; ++sc) {
     uint32_t key[kSelPer];
@@ -582,10 +592,14 @@ __device__ __forceinline__ uint32_t sel_block_sum(const uint32_t* cnt, int m, Se
 }
 
 // The selection's bit mask and its population per chunk. k == 0 selects nothing. merge: OR the bits taken here into
-// the mask words already written by sel_split_kernel (the keys above the prefix).
+// the mask words already written by sel_split_kernel (the keys above the prefix). comp: the selection of the n - r
+// smallest keys (in KeyF's complemented order, the n - r largest) when a two-stage selection took the r largest and
+// left its boundary {K*, e taken equal to K*} in sel_bound: its K* is ~K* and it takes the first (equal count - e)
+// keys equal to it (with no histogram passes; sel_eqcount_kernel with comp counts the equal keys first). Both take
+// equal keys lowest index first, so the two sets are complements except where the equal keys overlap.
 template <class KeyF>
 __global__ void __launch_bounds__(kSelThreads) sel_mark_kernel(KeyF kf, int n, SelWs ws, int sel, uint32_t k,
-                                                                int cand_sel, int merge) {
+                                                                int cand_sel, int merge, int comp) {
   __shared__ SelShared sh;
   __shared__ uint32_t weq[kSelThreads / 64];
   const int64_t row = blockIdx.y;
@@ -594,8 +608,15 @@ __global__ void __launch_bounds__(kSelThreads) sel_mark_kernel(KeyF kf, int n, S
   uint64_t* out = ws.mask + (row * kSelNSel + sel) * ws.words;
   uint32_t kstar = 0, pmask, rem = 0, eq_before = 0;
   if (k > 0) {
-    sel_state(ws.hist + (row * kSelNSel + sel) * 1024, 4, k, kstar, pmask, rem, sh);
-    eq_before = sel_block_sum(ws.eqcnt + (row * kSelNSel + sel) * ws.chunks, blockIdx.x, sh);
+    const uint32_t* eqc = ws.eqcnt + (row * kSelNSel + sel) * ws.chunks;
+    if (comp) {
+      const uint32_t* bnd = sel_bound(ws, row);
+      kstar = ~bnd[0];
+      rem = sel_block_sum(eqc, ws.chunks, sh) - bnd[1];
+    } else {
+      sel_state(ws.hist + (row * kSelNSel + sel) * 1024, 4, k, kstar, pmask, rem, sh);
+    }
+    eq_before = sel_block_sum(eqc, blockIdx.x, sh);
   }
   // sub-chunk by sub-chunk, in key order: this lane's keys above / equal to K* (one bit per step), the equal ones'
   // ranks counted over the earlier sub-chunks, waves and lanes
@@ -801,10 +822,11 @@ __global__ void __launch_bounds__(kTopkThreads) sel2_local_kernel(KeyF kf, int n
 }
 
 // Two-stage top-k, stage 2: the k largest of a row's m = chunks * k candidates (slot order = index order, lowest slot
-// first on equal keys), their indices written in ascending order.
+// first on equal keys), their indices written in ascending order; with `bound` set, also the row's K* and the number of
+// keys equal to it that were taken (sel_bound).
 template <int PER>
 __global__ void __launch_bounds__(kTopkThreads) sel2_merge_kernel(SelWs ws, int m, int k, int64_t* __restrict__ out,
-                                                                   int64_t out_rs) {
+                                                                   int64_t out_rs, int bound) {
   __shared__ TopkShared sh;
   const uint32_t* kp = ws.ckey + (int64_t)blockIdx.x * m;
   const int* ip = ws.cidx + (int64_t)blockIdx.x * m;
@@ -814,23 +836,28 @@ __global__ void __launch_bounds__(kTopkThreads) sel2_merge_kernel(SelWs ws, int 
   uint32_t key[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) key[j] = j < cnt ? kp[seg0 + j] : 0u;
-  const uint64_t take = radix_take<PER>(key, all, (uint32_t)k, sh);
+  const uint64_t take =
+      radix_take<PER>(key, all, (uint32_t)k, sh, bound ? sel_bound(ws, blockIdx.x) : nullptr);
   write_taken_gather(take, seg0, ip, out + (int64_t)blockIdx.x * out_rs, (uint32_t)k, sh);
 }
 
 // Both stages of a two-stage selection of k (chunks * k <= kSel2MaxCand) into out [rows] with row stride out_rs.
 template <class KeyF>
 void sel2_run(const KeyF& kf, int rows, int n, int k, const SelWs& ws, int cand_sel, int64_t* out, int64_t out_rs,
-              hipStream_t st) {
+              hipStream_t st, bool bound = false) {
+  const int bnd = bound ? 1 : 0;
   const int chunks = (n + kSel2Chunk - 1) / kSel2Chunk, m = chunks * k;
   hipLaunchKernelGGL(sel2_local_kernel<KeyF>, dim3((unsigned)chunks, (unsigned)rows), dim3(kTopkThreads), 0, st, kf, n,
                      k, ws, cand_sel);
   if (m <= 4 * kTopkThreads)
-    hipLaunchKernelGGL(sel2_merge_kernel<4>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, k, out, out_rs);
+    hipLaunchKernelGGL(sel2_merge_kernel<4>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, k, out, out_rs,
+                       bnd);
   else if (m <= 16 * kTopkThreads)
-    hipLaunchKernelGGL(sel2_merge_kernel<16>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, k, out, out_rs);
+    hipLaunchKernelGGL(sel2_merge_kernel<16>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, k, out, out_rs,
+                       bnd);
   else
-    hipLaunchKernelGGL(sel2_merge_kernel<64>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, k, out, out_rs);
+    hipLaunchKernelGGL(sel2_merge_kernel<64>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, k, out, out_rs,
+                       bnd);
 }
 
 // RoCo's output from its two two-stage selections: row r of out holds pick's `na` indices then recent's `nb`, each
@@ -870,15 +897,24 @@ template <class KeyF>
 void sel_run(const KeyF& kf, int rows, int n, const SelWs& ws, int sel, uint32_t k, int cand_sel, hipStream_t st) {
   const dim3 grid(ws.chunks, rows), block(kSelThreads);
   if (k == 0) {
-    hipLaunchKernelGGL(sel_mark_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, cand_sel, 0);
+    hipLaunchKernelGGL(sel_mark_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, cand_sel, 0, 0);
     return;
   }
   for (int ps = 0; ps < 2; ++ps)
     hipLaunchKernelGGL(sel_hist_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, ps, k, cand_sel);
   hipLaunchKernelGGL(sel_split_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, cand_sel);
   hipLaunchKernelGGL(sel_hist_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, 3, k, kSelPrefix);
-  hipLaunchKernelGGL(sel_eqcount_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, kSelPrefix);
-  hipLaunchKernelGGL(sel_mark_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, kSelPrefix, 1);
+  hipLaunchKernelGGL(sel_eqcount_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, kSelPrefix, 0);
+  hipLaunchKernelGGL(sel_mark_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, kSelPrefix, 1, 0);
+}
+
+// RoCo's `other` after a two-stage `recent` that left its boundary (sel_bound): the mask of the n - recent smallest
+// std keys, from one count of the keys equal to recent's K* and one marking pass.
+template <class KeyF>
+void sel_complement_run(const KeyF& kf, int rows, int n, const SelWs& ws, int sel, uint32_t k, hipStream_t st) {
+  const dim3 grid(ws.chunks, rows), block(kSelThreads);
+  hipLaunchKernelGGL(sel_eqcount_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, kSelAll, 1);
+  hipLaunchKernelGGL(sel_mark_kernel<KeyF>, grid, block, 0, st, kf, n, ws, sel, k, kSelAll, 0, 1);
 }
 
 void sel_zero_hist(const SelWs& ws, int rows, hipStream_t st) {
@@ -1007,11 +1043,15 @@ extern "C" int dgg_roco_select_ws(const float* score, const float* sq_score, int
     // recent and pick in two stages (pick among other's mask), other in passes; the two index lists are written to
     // out's rows (pick first) and merged in place
     const int64_t rs = budget + recent;
-    sel_zero_hist(ws, R, st);
-    if (recent > 0) sel2_run(KeyStd{score, sq_score, N, rcp, 0}, R, N, (int)recent, ws, kSelAll, out_idx + budget, rs, st);
+    if (recent > 0)  // roco.py:56, leaving its boundary for `other`
+      sel2_run(KeyStd{score, sq_score, N, rcp, 0}, R, N, (int)recent, ws, kSelAll, out_idx + budget, rs, st, true);
     if (budget > 0) {
-      sel_run(KeyStd{score, sq_score, N, rcp, 1}, R, N, ws, 1, (uint32_t)(n - recent), kSelAll, st);  // roco.py:55
-      sel2_run(KeyMean{score, N, rcp}, R, N, (int)budget, ws, 1, out_idx, rs, st);                  // roco.py:57-58
+      if (recent > 0) {  // roco.py:55 from recent's boundary, then roco.py:57-58 among its keys
+        sel_complement_run(KeyStd{score, sq_score, N, rcp, 1}, R, N, ws, 1, (uint32_t)(n - recent), st);
+        sel2_run(KeyMean{score, N, rcp}, R, N, (int)budget, ws, 1, out_idx, rs, st);
+      } else {  // `other` is every key
+        sel2_run(KeyMean{score, N, rcp}, R, N, (int)budget, ws, kSelAll, out_idx, rs, st);
+      }
     }
     if (budget > 0 && recent > 0)
       hipLaunchKernelGGL(roco_merge_kernel, dim3((unsigned)rows), dim3(256), 0, st, out_idx, (int)budget, (int)recent);

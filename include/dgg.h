@@ -239,7 +239,8 @@ int dgg_roco_select(const float* score, const float* sq_score, int64_t rows, int
 
 /* Rows of more than 65536 keys (up to 2^26): dgg_topk_select and dgg_roco_select with the same results, computed
  * by many workgroups per row (a top-k with ceil(n / 16384) * k <= 65536 in two stages, a chunk-wise top-k and a
- * merge, reading the row once; others in radix passes) through a caller-provided workspace of
+ * merge, reading the row once; others in radix passes; RoCo's `other` from the boundary of a two-stage `recent`,
+ * in two reads of the row) through a caller-provided workspace of
  * dgg_select_workspace_bytes(rows, n) bytes (0 for n <= 65536, where these calls are dgg_topk_select /
  * dgg_roco_select and ignore the workspace), 256-byte aligned; rows <= 65535 when n > 65536. No counterpart in the
  * reference beyond the torch.topk calls they replace (models/h2o.py:51, models/snapkv.py:51, models/kf.py:54,

@@ -285,9 +285,11 @@ constexpr int kSelChunk = kSelWaveSpan * (kSelThreads / 64);  // keys per workgr
 constexpr int kSelMaxN = 1 << 26;
 constexpr int kSelNSel = 3;                                 // selections a workspace holds (RoCo's three)
 // Two-stage top-k (small k): each 1024-thread workgroup takes the k largest of its kSel2Chunk keys, then one workgroup
-// per row selects among the chunks' candidates (at most kSel2MaxCand, held in registers by topk's kernels). (32 keys
-// per lane instead of 16 spills: 124 VGPRs and 164 SGPRs.)
-constexpr int kSel2Per = 16;                                // keys per lane in the first stage
+// per row selects among the chunks' candidates (at most kSel2MaxCand, held in registers by topk's kernels). 8 keys per
+// lane fit 64 VGPRs, so two workgroups share a CU (measured on MI355X, top-256 of 32 rows: 186-187 against 205 us at
+// 1,048,576 keys, 31.8 against 33.4 us at 131,072, for 16 keys per lane at 128 VGPRs and one workgroup per CU; 32
+// keys per lane spill 124 VGPRs and 164 SGPRs).
+constexpr int kSel2Per = 8;                                 // keys per lane in the first stage
 constexpr int kSel2Chunk = 64 * kSel2Per * kTopkWaves;      // keys per workgroup
 constexpr int kSel2MaxCand = 64 * kTopkThreads;             // candidates per row
 
@@ -718,7 +720,8 @@ __global__ void __launch_bounds__(kSelThreads) sel_emit_kernel(int n, SelWs ws, 
 // direction; NaN maps to the top) or, for KeyScores' smallest-first keys, where NaN maps to 0, without a mask only
 // the last chunk pads, after every other slot, and among equal keys the lowest slot goes first.
 template <class KeyF>
-__global__ void __launch_bounds__(kTopkThreads) sel2_local_kernel(KeyF kf, int n, int k, SelWs ws, int cand_sel) {
+__global__ void __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8)))
+sel2_local_kernel(KeyF kf, int n, int k, SelWs ws, int cand_sel) {
   constexpr int kSel2Span = 64 * kSel2Per;  // keys per wave
   __shared__ TopkShared sh;
   __shared__ uint32_t wcnt[kTopkWaves];
@@ -862,7 +865,9 @@ void sel2_run(const KeyF& kf, int rows, int n, int k, const SelWs& ws, int cand_
 
 // RoCo's output from its two two-stage selections: row r of out holds pick's `na` indices then recent's `nb`, each
 // ascending; they are merged in place into one ascending list (an index in both written twice). One workgroup per
-// row; both lists go through LDS as 32-bit indices (n <= 2^26), na + nb <= kRocoMergeMax.
+// row; both lists go through LDS as 32-bit indices (n <= 2^26), na + nb <= kRocoMergeMax. (Rows of more than 65,536
+// keys have at least 9 chunks, so each list of the two-stage form holds at most 65,536 / 9 indices and the limit
+// holds by itself; the host checks it anyway.)
 constexpr int kRocoMergeMax = 16384;
 __global__ void __launch_bounds__(256) roco_merge_kernel(int64_t* __restrict__ out, int na, int nb) {
   __shared__ int la[kRocoMergeMax];

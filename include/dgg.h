@@ -238,7 +238,7 @@ int dgg_roco_select(const float* score, const float* sq_score, int64_t rows, int
                     int64_t budget, int64_t* out_idx, void* stream);
 
 /* Rows of more than 65536 keys (up to 2^26): dgg_topk_select and dgg_roco_select with the same results, computed
- * by many workgroups per row (a top-k with ceil(n / 16384) * k <= 65536 in two stages, a chunk-wise top-k and a
+ * by many workgroups per row (a top-k with ceil(n / 8192) * k <= 65536 in two stages, a chunk-wise top-k and a
  * merge, reading the row once; others in radix passes; RoCo's `other` from the boundary of a two-stage `recent`,
  * in two reads of the row) through a caller-provided workspace of
  * dgg_select_workspace_bytes(rows, n) bytes (0 for n <= 65536, where these calls are dgg_topk_select /

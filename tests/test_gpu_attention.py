@@ -474,8 +474,8 @@ def test_topk_long_rows_continuous_values(gpu, n):
 
 
 def test_topk_long_rows_two_stage_boundary(gpu):
-    # at 1,048,576 keys (64 chunks of 16,384) k = 1,024 is the largest k of the two-stage selection (64 x 1,024
-    # candidates, the merge's 64-per-thread form) and k = 1,025 the smallest of the pass form; ties across chunk
+    # at 1,048,576 keys (128 chunks of 8,192) k = 512 is the largest k of the two-stage selection (128 x 512
+    # candidates, the merge's 64-per-thread form) and k = 513 the smallest of the pass form; ties across chunk
     # borders (a value repeated every 1,000 keys) decide both
     n = 1048576
     rng = np.random.default_rng(11)
@@ -483,7 +483,7 @@ def test_topk_long_rows_two_stage_boundary(gpu):
     vals[0, ::1000] = 3.5
     vals[1] = np.round(vals[1] * 4) / 4
     x = torch.from_numpy(vals).to(gpu)
-    for k in (1024, 1025):
+    for k in (512, 513):
         progress(f"topk two-stage boundary n={n} k={k}")
         for largest in (True, False):
             got = A.topk_indices(x, k, largest=largest).cpu().numpy()
@@ -494,12 +494,12 @@ def test_topk_long_rows_two_stage_boundary(gpu):
                                                    (70000, 3, 0, 69999), (70000, 3, 70000, 0),
                                                    (131072, 4096, 0, 700), (131072, 4096, 700, 0),
                                                    (200000, 50, 1000, 3000),
-                                                   (65600, 7, 3277, 13107), (65600, 7, 3278, 13107)])
+                                                   (65600, 7, 3000, 7281), (65600, 7, 3000, 7282)])
 def test_roco_select_rows_longer_than_65536(gpu, n, q_len, recent, budget):
     # RoCo's three chained selections over several workgroups per row, with ties and NaN std (negative variance);
-    # recent and pick in two stages where chunks * k allows (the first and the fifth to eighth cases), else all in
-    # passes. The last two sit at the in-place merge's limit of 16,384 indices per row (5 chunks x 13,107 candidates
-    # fits the two-stage form): exactly at it, then one index past it (all in passes)
+    # recent and pick in two stages where chunks * k allows (the first and the fifth to eighth cases), with `other`
+    # from recent's boundary, else all in passes. The last two sit at the two-stage form's candidate limit (9 chunks
+    # of 8,192 keys x 7,281 = 65,529 candidates for `pick`), exactly at it and one past it (all in passes)
     rng = np.random.default_rng(n + recent)
     s1 = rng.integers(0, 50, size=(2, n)).astype(np.float32)
     s2 = rng.integers(0, 80, size=(2, n)).astype(np.float32) / 2.0

@@ -858,6 +858,9 @@ void sel2_run(const KeyF& kf, int rows, int n, int k, const SelWs& ws, int cand_
   else if (m <= 16 * kTopkThreads)
     hipLaunchKernelGGL(sel2_merge_kernel<16>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, k, out, out_rs,
                        bnd);
+  else if (m <= 32 * kTopkThreads)
+    hipLaunchKernelGGL(sel2_merge_kernel<32>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, k, out, out_rs,
+                       bnd);
   else
     hipLaunchKernelGGL(sel2_merge_kernel<64>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, k, out, out_rs,
                        bnd);

@@ -274,9 +274,10 @@ __global__ void __launch_bounds__(kTopkThreads) roco_select_kernel(const float* 
 // Steps 1 and 2 read every key (three reads of the row); steps 3-5 load only the keys of mask words that hold a
 // prefix-mask bit, which for scores in general is a small share of the row (all of it when every key is equal).
 // RoCo chains three selections: `recent` (largest std), `other` (smallest std), `pick` (largest mean among the
-// candidates of `other`'s mask), then writes pick and recent merged. `recent` and `pick` take the two-stage form when
-// both fit it (their sorted lists then go to the output rows and roco_merge_kernel merges them); `other`, whose k is
-// n - recent, runs in passes.
+// candidates of `other`'s mask), then writes pick and recent merged. When `recent` and `pick` both fit the two-stage
+// form, they take it (their sorted lists go to the output rows and roco_merge_kernel merges them), and `other`, whose
+// k is n - recent, is built from `recent`'s boundary by steps 4 and 5 alone (sel_complement_run); otherwise all three
+// run in passes.
 // ------------------------------------------------------------------------------------------------
 constexpr int kSelThreads = 256;
 constexpr int kSelPer = 16;                                 // keys per lane per chunk, loaded back to back
@@ -287,8 +288,8 @@ constexpr int kSelNSel = 3;                                 // selections a work
 // Two-stage top-k (small k): each 1024-thread workgroup takes the k largest of its kSel2Chunk keys, then one workgroup
 // per row selects among the chunks' candidates (at most kSel2MaxCand, held in registers by topk's kernels). 8 keys per
 // lane fit 64 VGPRs, so two workgroups share a CU (measured on MI355X, top-256 of 32 rows: 186-187 against 205 us at
-// 1,048,576 keys, 31.8 against 33.4 us at 131,072, for 16 keys per lane at 128 VGPRs and one workgroup per CU; 32
-// keys per lane spill 124 VGPRs and 164 SGPRs).
+// 1,048,576 keys, 31.8 against 33.4 us at 131,072, for 16 keys per lane at 128 VGPRs and one workgroup per CU, both
+// with the 64-per-lane merge; 32 keys per lane spill 124 VGPRs and 164 SGPRs).
 constexpr int kSel2Per = 8;                                 // keys per lane in the first stage
 constexpr int kSel2Chunk = 64 * kSel2Per * kTopkWaves;      // keys per workgroup
 constexpr int kSel2MaxCand = 64 * kTopkThreads;             // candidates per row

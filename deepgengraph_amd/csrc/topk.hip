@@ -293,6 +293,7 @@ constexpr int kSelNSel = 3;                                 // selections a work
 constexpr int kSel2Per = 8;                                 // keys per lane in the first stage
 constexpr int kSel2Chunk = 64 * kSel2Per * kTopkWaves;      // keys per workgroup
 constexpr int kSel2MaxCand = 64 * kTopkThreads;             // candidates per row
+constexpr int kSel2C2 = 16384;  // second-level candidates per row (groups * k <= 65,536 / 8 + k, see sel2_run)
 
 struct SelWs {
   uint32_t* hist;   // [rows][kSelNSel][4][256]
@@ -302,6 +303,8 @@ struct SelWs {
   uint64_t* pre;    // [rows][words]: the prefix mask of the selection in progress
   uint32_t* ckey;   // two-stage candidates, [rows][m] with m = chunks * k <= kSel2MaxCand (room for kSel2MaxCand per row)
   int* cidx;        // their indices, same layout
+  uint32_t* c2key;  // the group level's candidates, [rows][kSel2C2]
+  int* c2idx;       // their indices
   int chunks, words;
   int spc;          // kSelChunk-key sub-chunks per workgroup (a chunk is spc * kSelChunk keys)
 };
@@ -321,6 +324,7 @@ inline int64_t sel_layout(int64_t rows, int64_t n, void* base, SelWs* ws) {
   const int64_t mask_b = sel_align(rows * kSelNSel * words * 8);
   const int64_t pre_b = sel_align(rows * words * 8);
   const int64_t cand_b = sel_align(rows * (int64_t)kSel2MaxCand * 4);
+  const int64_t cand2_b = sel_align(rows * (int64_t)kSel2C2 * 4);
   if (ws != nullptr) {
     char* c = static_cast<char*>(base);
     ws->hist = reinterpret_cast<uint32_t*>(c);
@@ -330,11 +334,13 @@ inline int64_t sel_layout(int64_t rows, int64_t n, void* base, SelWs* ws) {
     ws->pre = reinterpret_cast<uint64_t*>(c + hist_b + 2 * cnt_b + mask_b);
     ws->ckey = reinterpret_cast<uint32_t*>(c + hist_b + 2 * cnt_b + mask_b + pre_b);
     ws->cidx = reinterpret_cast<int*>(c + hist_b + 2 * cnt_b + mask_b + pre_b + cand_b);
+    ws->c2key = reinterpret_cast<uint32_t*>(c + hist_b + 2 * cnt_b + mask_b + pre_b + 2 * cand_b);
+    ws->c2idx = reinterpret_cast<int*>(c + hist_b + 2 * cnt_b + mask_b + pre_b + 2 * cand_b + cand2_b);
     ws->chunks = (int)chunks;
     ws->words = (int)words;
     ws->spc = (int)spc;
   }
-  return hist_b + 2 * cnt_b + mask_b + pre_b + 2 * cand_b;
+  return hist_b + 2 * cnt_b + mask_b + pre_b + 2 * cand_b + 2 * cand2_b;
 }
 
 // Key sources: element j of row `row` as an order key (larger = taken first), in two steps: load() reads what the
@@ -825,15 +831,17 @@ sel2_local_kernel(KeyF kf, int n, int k, SelWs ws, int cand_sel) {
   }
 }
 
-// Two-stage top-k, stage 2: the k largest of a row's m = chunks * k candidates (slot order = index order, lowest slot
-// first on equal keys), their indices written in ascending order; with `bound` set, also the row's K* and the number of
-// keys equal to it that were taken (sel_bound).
+// Two-stage top-k, stage 2: the k largest of a row's m candidates (row stride crs; slot order = index order, lowest
+// slot first on equal keys), their indices written in ascending order; with `bound` set, also the row's K* and the
+// number of keys equal to it that were taken (sel_bound).
 template <int PER>
-__global__ void __launch_bounds__(kTopkThreads) sel2_merge_kernel(SelWs ws, int m, int k, int64_t* __restrict__ out,
-                                                                   int64_t out_rs, int bound) {
+__global__ void __launch_bounds__(kTopkThreads) sel2_merge_kernel(SelWs ws, const uint32_t* __restrict__ ckey,
+                                                                   const int* __restrict__ cidx, int64_t crs, int m,
+                                                                   int k, int64_t* __restrict__ out, int64_t out_rs,
+                                                                   int bound) {
   __shared__ TopkShared sh;
-  const uint32_t* kp = ws.ckey + (int64_t)blockIdx.x * m;
-  const int* ip = ws.cidx + (int64_t)blockIdx.x * m;
+  const uint32_t* kp = ckey + (int64_t)blockIdx.x * crs;
+  const int* ip = cidx + (int64_t)blockIdx.x * crs;
   int seg0, cnt;
   uint64_t all;
   segment(m, seg0, cnt, all);
@@ -845,6 +853,46 @@ __global__ void __launch_bounds__(kTopkThreads) sel2_merge_kernel(SelWs ws, int 
   write_taken_gather(take, seg0, ip, out + (int64_t)blockIdx.x * out_rs, (uint32_t)k, sh);
 }
 
+// The group level between the two stages, for rows with many chunks: workgroup (g, row) takes the k largest of the
+// candidates in slots [g * gslots, (g + 1) * gslots) of the row (whole chunks, so at least k of them) and writes them
+// as (key, index) in slot order to slots [g * k, (g + 1) * k) of the row's group-level candidates. The groups of a
+// row run side by side instead of one workgroup per row walking all of them.
+template <int PER>
+__global__ void __launch_bounds__(kTopkThreads) sel2_group_kernel(SelWs ws, int m, int k, int gslots) {
+  __shared__ TopkShared sh;
+  const int64_t row = blockIdx.y;
+  const int s0 = blockIdx.x * gslots;
+  const int cnt_g = min(gslots, m - s0);
+  const uint32_t* kp = ws.ckey + row * m + s0;
+  const int* ip = ws.cidx + row * m + s0;
+  int seg0, cnt;
+  uint64_t all;
+  segment(cnt_g, seg0, cnt, all);
+  uint32_t key[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) key[j] = j < cnt ? kp[seg0 + j] : 0u;
+  uint64_t take = radix_take<PER>(key, all, (uint32_t)k, sh);
+  uint32_t tot;
+  uint32_t pos = block_exclusive_scan(__popcll(take), sh.wsum, tot);
+  uint32_t* ok = ws.c2key + row * kSel2C2 + (int64_t)blockIdx.x * k;
+  int* oi = ws.c2idx + row * kSel2C2 + (int64_t)blockIdx.x * k;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    if ((take >> j) & 1) {
+      ok[pos] = key[j];
+      oi[pos] = ip[seg0 + j];
+      ++pos;
+    }
+  }
+}
+
+template <int PER>
+void sel2_merge_launch(const SelWs& ws, const uint32_t* ck, const int* ci, int64_t crs, int rows, int m, int k,
+                       int64_t* out, int64_t out_rs, int bnd, hipStream_t st) {
+  hipLaunchKernelGGL(sel2_merge_kernel<PER>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, ck, ci, crs, m, k,
+                     out, out_rs, bnd);
+}
+
 // Both stages of a two-stage selection of k (chunks * k <= kSel2MaxCand) into out [rows] with row stride out_rs.
 template <class KeyF>
 void sel2_run(const KeyF& kf, int rows, int n, int k, const SelWs& ws, int cand_sel, int64_t* out, int64_t out_rs,
@@ -853,18 +901,28 @@ void sel2_run(const KeyF& kf, int rows, int n, int k, const SelWs& ws, int cand_
   const int chunks = (n + kSel2Chunk - 1) / kSel2Chunk, m = chunks * k;
   hipLaunchKernelGGL(sel2_local_kernel<KeyF>, dim3((unsigned)chunks, (unsigned)rows), dim3(kTopkThreads), 0, st, kf, n,
                      k, ws, cand_sel);
-  if (m <= 4 * kTopkThreads)
-    hipLaunchKernelGGL(sel2_merge_kernel<4>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, k, out, out_rs,
-                       bnd);
-  else if (m <= 16 * kTopkThreads)
-    hipLaunchKernelGGL(sel2_merge_kernel<16>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, k, out, out_rs,
-                       bnd);
-  else if (m <= 32 * kTopkThreads)
-    hipLaunchKernelGGL(sel2_merge_kernel<32>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, k, out, out_rs,
-                       bnd);
-  else
-    hipLaunchKernelGGL(sel2_merge_kernel<64>, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, ws, m, k, out, out_rs,
-                       bnd);
+  const uint32_t* ck = ws.ckey;
+  const int* ci = ws.cidx;
+  int64_t crs = m;
+  int mm = m;
+  if (k <= 512 && m > 16 * kTopkThreads) {
+    // groups of whole chunks, at most 4 * kTopkThreads candidates each (at least 8 chunks: groups * k stays within
+    // 65,536 / 8 + k <= kSel2C2). Measured on MI355X, top-256 of 32 x 1,048,576 (8 groups): 159.6 against 177.3 us
+    // with the one-workgroup-per-row merge; RoCo's `pick` at 32 x 131,072 (2 groups) lost 3 % on the extra launch,
+    // hence the group level only where the single merge would hold more than 16 candidates per lane.
+    const int gslots = (4 * kTopkThreads / k) * k;
+    const int groups = (m + gslots - 1) / gslots;
+    hipLaunchKernelGGL(sel2_group_kernel<4>, dim3((unsigned)groups, (unsigned)rows), dim3(kTopkThreads), 0, st, ws, m,
+                       k, gslots);
+    ck = ws.c2key;
+    ci = ws.c2idx;
+    crs = kSel2C2;
+    mm = groups * k;
+  }
+  if (mm <= 4 * kTopkThreads) sel2_merge_launch<4>(ws, ck, ci, crs, rows, mm, k, out, out_rs, bnd, st);
+  else if (mm <= 16 * kTopkThreads) sel2_merge_launch<16>(ws, ck, ci, crs, rows, mm, k, out, out_rs, bnd, st);
+  else if (mm <= 32 * kTopkThreads) sel2_merge_launch<32>(ws, ck, ci, crs, rows, mm, k, out, out_rs, bnd, st);
+  else sel2_merge_launch<64>(ws, ck, ci, crs, rows, mm, k, out, out_rs, bnd, st);
 }
 
 // RoCo's output from its two two-stage selections: row r of out holds pick's `na` indices then recent's `nb`, each

@@ -1,0 +1,104 @@
+"""Seeded random sweeps over the launch space of the forward and selection entry points, against the CPU oracle at the
+tolerances of test_gpu_attention.py (bf16 2e-2 abs / 1e-2 rel, fp16 1e-2 / 5e-3; index sets identical). Each seed
+draws one configuration: head_dim, grouped query heads, causal / window / soft-cap, ragged and unequal Sq / Sk (so
+one-row calls go to the decode kernels and short query blocks to the split-KV kernels, as attention() routes them),
+dtype; rows of tie-heavy, NaN-holding or continuous scores, of 1 to 70,000 keys, for the selections. The case is
+printed before it runs."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close, progress
+from deepgengraph_amd import attention as A
+from oracle import attention as oa
+from oracle import selection as osel
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.bfloat16: (2e-2, 1e-2), torch.float16: (1e-2, 5e-3)}
+
+
+def _draw_attention_case(seed):
+    rng = np.random.default_rng(1000 + seed)
+    D = int(rng.choice([64, 128, 256]))
+    Hkv = int(rng.choice([1, 2]))
+    G = int(rng.choice([1, 2, 4]))
+    B = int(rng.choice([1, 2]))
+    shape = rng.integers(0, 4)
+    if shape == 0:  # one query row over a cache (decode kernels when Sk >= 256)
+        Sq, Sk = 1, int(rng.integers(1, 1500))
+    elif shape == 1:  # a short query block (split-KV kernels over >= 512 keys)
+        Sq, Sk = int(rng.integers(2, 65)), int(rng.integers(64, 1500))
+    else:
+        Sq, Sk = int(rng.integers(1, 600)), int(rng.integers(1, 600))
+    causal = bool(rng.integers(0, 2))
+    softcap = float(rng.choice([0.0, 0.0, 20.0, 50.0]))
+    window = int(rng.integers(1, Sk + 1)) if causal and rng.integers(0, 3) == 0 else 0
+    dtype = torch.bfloat16 if rng.integers(0, 2) else torch.float16
+    return B, Sq, Sk, Hkv * G, Hkv, D, dtype, causal, softcap, window
+
+
+@pytest.mark.parametrize("seed", range(64))
+def test_attention_random_launches_match_oracle(gpu, seed):
+    B, Sq, Sk, Hq, Hkv, D, dtype, causal, softcap, window = _draw_attention_case(seed)
+    what = f"seed {seed}: B{B} Sq{Sq} Sk{Sk} H{Hq}/{Hkv} D{D} {dtype} causal={causal} cap={softcap} win={window}"
+    progress(what)
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Sq, Hq, D, generator=g).to(dtype)
+    k = torch.randn(B, Sk, Hkv, D, generator=g).to(dtype)
+    v = torch.randn(B, Sk, Hkv, D, generator=g).to(dtype)
+    ref, ref_lse = oa.attention(q, k, v, causal=causal, softcap=softcap or None, window=window or None,
+                                return_lse=True)
+    out, lse = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), causal=causal, softcap=softcap, window=window,
+                           return_lse=True)
+    assert_close(out.cpu().float(), ref.float(), *TOL[dtype], what + " out")
+    lse_c = lse.cpu()
+    fin = torch.isfinite(ref_lse)
+    assert torch.equal(torch.isfinite(lse_c), fin), what + " lse -inf pattern"
+    assert_close(lse_c[fin], ref_lse[fin], 2e-2, 1e-2, what + " lse")
+
+
+def _draw_rows(rng, rows, n):
+    kind = int(rng.integers(0, 4))
+    if kind == 0:  # few distinct values: ties decide
+        return (rng.integers(0, 7, size=(rows, n)).astype(np.float32) - 3.0) / 2.0, "ties"
+    if kind == 1:  # signed zeros, infinities and NaN among ties
+        pool = np.array([0.0, -0.0, 1.0, -1.0, np.inf, -np.inf, np.nan, 2.5], dtype=np.float32)
+        return rng.choice(pool, size=(rows, n)), "specials"
+    if kind == 2:  # a narrow band: the keys share their leading bytes
+        return (1.0 + rng.random((rows, n)) * 1e-3).astype(np.float32), "band"
+    return rng.standard_normal((rows, n)).astype(np.float32), "normal"
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_topk_random_rows_match_oracle(gpu, seed):
+    rng = np.random.default_rng(2000 + seed)
+    rows = int(rng.integers(1, 6))
+    n = int(rng.choice([rng.integers(1, 5000), rng.integers(5000, 65537), rng.integers(65537, 70001)]))
+    k = int(rng.choice([1, rng.integers(1, n + 1), min(n, 256), n]))
+    largest = bool(rng.integers(0, 2))
+    vals, kind = _draw_rows(rng, rows, n)
+    what = f"seed {seed}: {rows} x {n} {kind} k={k} largest={largest}"
+    progress(what)
+    got = A.topk_indices(torch.from_numpy(vals).to(gpu), k, largest=largest).cpu().numpy()
+    np.testing.assert_array_equal(got, osel.topk_indices(vals, k, largest), err_msg=what)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_roco_select_random_rows_match_oracle(gpu, seed):
+    rng = np.random.default_rng(3000 + seed)
+    rows = int(rng.integers(1, 4))
+    n = int(rng.choice([rng.integers(1, 65537), rng.integers(65537, 70001)]))
+    q_len = int(rng.integers(1, 5000))
+    recent = int(rng.choice([0, rng.integers(0, n + 1), min(n, 256)]))
+    budget = int(rng.choice([0, rng.integers(0, n - recent + 1), min(n - recent, 512)]))
+    if rng.integers(0, 2):  # integer sums: ties, and negative variances (NaN std)
+        s1 = rng.integers(0, 40, size=(rows, n)).astype(np.float32)
+        s2 = rng.integers(0, 60, size=(rows, n)).astype(np.float32) / 2.0
+    else:
+        s1 = rng.random((rows, n)).astype(np.float32) * q_len
+        s2 = s1 * s1 / q_len + rng.random((rows, n)).astype(np.float32)
+    what = f"seed {seed}: {rows} x {n} q_len={q_len} recent={recent} budget={budget}"
+    progress(what)
+    got = A.roco_select(torch.from_numpy(s1).to(gpu), torch.from_numpy(s2).to(gpu), q_len, recent, budget)
+    np.testing.assert_array_equal(got.cpu().numpy(), osel.roco_select(s1, s2, q_len, recent, budget), err_msg=what)

@@ -3,7 +3,8 @@ tolerances of test_gpu_attention.py (bf16 2e-2 abs / 1e-2 rel, fp16 1e-2 / 5e-3;
 draws one configuration: head_dim, grouped query heads, causal / window / soft-cap, ragged and unequal Sq / Sk (so
 one-row calls go to the decode kernels and short query blocks to the split-KV kernels, as attention() routes them),
 dtype; rows of tie-heavy, NaN-holding or continuous scores, of 1 to 70,000 keys, for the selections. The case is
-printed before it runs."""
+printed before it runs. The column-score cases compare with the reference probabilities of
+test_gpu_attention.py (1e-3 rel)."""
 import numpy as np
 import pytest
 import torch
@@ -102,3 +103,39 @@ def test_roco_select_random_rows_match_oracle(gpu, seed):
     progress(what)
     got = A.roco_select(torch.from_numpy(s1).to(gpu), torch.from_numpy(s2).to(gpu), q_len, recent, budget)
     np.testing.assert_array_equal(got.cpu().numpy(), osel.roco_select(s1, s2, q_len, recent, budget), err_msg=what)
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_colscore_random_launches_match_reference(gpu, seed):
+    # the column-score pass (H2O sums, RoCo's sums and sums of squares) after the lse-writing forward with the
+    # reference's score rounding, against the reference's probabilities at the column-sum contract (1e-3 rel)
+    from deepgengraph_amd import _lib
+    from test_gpu_attention import _colsum_check, _colsum_reference
+
+    rng = np.random.default_rng(4000 + seed)
+    D = int(rng.choice([64, 128, 256]))
+    Hkv = int(rng.choice([1, 2]))
+    Hq = Hkv * int(rng.choice([1, 2]))
+    Sq, Sk = int(rng.integers(1, 700)), int(rng.integers(1, 700))
+    causal = bool(rng.integers(0, 2))
+    sumsq = bool(rng.integers(0, 2))
+    softcap = 0.0 if sumsq else float(rng.choice([0.0, 0.0, 30.0]))
+    window = int(rng.integers(1, Sk + 1)) if causal and rng.integers(0, 3) == 0 else 0
+    dtype = torch.bfloat16 if rng.integers(0, 2) else torch.float16
+    base2 = bool(rng.integers(0, 2))
+    what = (f"seed {seed}: Sq{Sq} Sk{Sk} H{Hq}/{Hkv} D{D} {dtype} causal={causal} cap={softcap} win={window} "
+            f"base2={base2} sumsq={sumsq}")
+    progress(what)
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(1, Sq, Hq, D, generator=g).to(dtype)
+    k = torch.randn(1, Sk, Hkv, D, generator=g).to(dtype)
+    v = torch.randn(1, Sk, Hkv, D, generator=g).to(dtype)
+    kw = dict(causal=causal, window=window, lse_base2=base2)
+    _, lse = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), return_lse=True, ref_rounding=True, softcap=softcap, **kw)
+    if sumsq:
+        s1, s2 = A.attention_colscore(q.to(gpu), k.to(gpu), lse, epilogue=_lib.COL_SUM_SQ, ref_rounding=True, **kw)
+        _colsum_check(s1.cpu(), _colsum_reference(q, k, causal, 0.0, window).float(), what + " sum")
+        _colsum_check(s2.cpu(), _colsum_reference(q, k, causal, 0.0, window, power=2).float(), what + " sum of squares")
+    else:
+        cs = A.attention_colsum(q.to(gpu), k.to(gpu), lse, softcap=softcap, **kw).cpu()
+        _colsum_check(cs, _colsum_reference(q, k, causal, softcap, window).float(), what + " sum")

@@ -2,7 +2,8 @@
 tolerances of test_gpu_attention.py (bf16 2e-2 abs / 1e-2 rel, fp16 1e-2 / 5e-3; index sets identical). Each seed
 draws one configuration: head_dim, grouped query heads, causal / window / soft-cap, ragged and unequal Sq / Sk (so
 one-row calls go to the decode kernels and short query blocks to the split-KV kernels, as attention() routes them),
-dtype; rows of tie-heavy, NaN-holding or continuous scores, of 1 to 70,000 keys, for the selections. The case is
+dtype; rows of tie-heavy, NaN-holding or continuous scores, of 1 to 70,000 keys, for the selections; drawn widths
+and dtypes for the elementwise ops. The case is
 printed before it runs. The column-score cases compare with the reference probabilities of
 test_gpu_attention.py (1e-3 rel)."""
 import numpy as np
@@ -139,3 +140,62 @@ def test_colscore_random_launches_match_reference(gpu, seed):
     else:
         cs = A.attention_colsum(q.to(gpu), k.to(gpu), lse, softcap=softcap, **kw).cpu()
         _colsum_check(cs, _colsum_reference(q, k, causal, softcap, window).float(), what + " sum")
+
+
+def _draw_width(rng):
+    """A row width: a multiple of 8 (the vector paths) or not (the scalar ones), small or wide."""
+    w = int(rng.integers(1, 8193))
+    return w - w % 8 if rng.integers(0, 2) and w >= 8 else w
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_elementwise_random_shapes_match_oracle(gpu, seed):
+    # RMSNorm, fused add + RMSNorm, SiLU-and-mul and the online rotary (csrc/norm.cu, activation.cu,
+    # pos_encoding.cu) on drawn shapes and dtypes, through the csrc-compatible wrappers
+    from deepgengraph_amd import ops
+    from oracle import elementwise as oe
+
+    rng = np.random.default_rng(5000 + seed)
+    dtype = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(0, 3))]
+    tol = {torch.bfloat16: (2e-2, 1e-2), torch.float16: (1e-2, 5e-3), torch.float32: (1e-5, 1e-5)}[dtype]
+    g = torch.Generator().manual_seed(seed)
+    rows, hidden = int(rng.integers(1, 300)), _draw_width(rng)
+    what = f"seed {seed}: rms_norm {rows}x{hidden} {dtype}"
+    progress(what)
+    x = torch.randn(rows, hidden, generator=g).to(dtype)
+    r = torch.randn(rows, hidden, generator=g).to(dtype)
+    w = (1.0 + 0.02 * torch.randn(hidden, generator=g)).to(dtype)
+    out = torch.empty(rows, hidden, dtype=dtype, device=gpu)
+    ops.rms_norm(out, x.to(gpu), w.to(gpu), 1e-6)
+    assert_close(out.cpu().float(), oe.rms_norm(x, w, 1e-6).float(), *tol, what)
+    ref_out, ref_res = oe.fused_add_rms_norm(x, r, w, 1e-6)
+    xg, rg = x.to(gpu), r.to(gpu)
+    ops.fused_add_rms_norm(xg, rg, w.to(gpu), 1e-6)
+    assert torch.equal(rg.cpu(), ref_res), what + ": fused residual = T(input + residual) must be exact"
+    assert_close(xg.cpu().float(), ref_out.float(), *tol, what + " fused")
+
+    arows, d = int(rng.integers(1, 300)), _draw_width(rng)
+    what = f"seed {seed}: silu_and_mul {arows}x{d} {dtype}"
+    progress(what)
+    gu = (3.0 * torch.randn(arows, 2 * d, generator=g)).to(dtype)
+    act = torch.empty(arows, d, dtype=dtype, device=gpu)
+    ops.silu_and_mul(act, gu.to(gpu))
+    assert_close(act.cpu().float(), oe.silu_and_mul(gu).float(), *tol, what)
+
+    tokens, hk = int(rng.integers(1, 200)), int(rng.integers(1, 5))
+    # head_dim: multiples of 16 up to 256 (the wrapper's range; the reference asserts 128, pos_encoding.cu:193)
+    hq, D = hk * int(rng.integers(1, 4)), 16 * int(rng.integers(1, 17))
+    pad = int(rng.choice([0, 0, 3, 8]))
+    what = f"seed {seed}: rotary T{tokens} {hq}/{hk} D{D} pad{pad} {dtype}"
+    progress(what)
+    qkv = torch.randn(tokens, (hq + 2 * hk) * D + pad, generator=g).to(dtype)
+    pos = torch.randint(0, 8192, (tokens,), generator=g, dtype=torch.int32)
+    q, k = qkv[:, : hq * D], qkv[:, hq * D: (hq + hk) * D]
+    ref_q, ref_k = oe.rotary_embedding_online(pos, q.contiguous(), k.contiguous(), D, 10000.0)
+    qkv_g = qkv.to(gpu)
+    gq, gk = qkv_g[:, : hq * D], qkv_g[:, hq * D: (hq + hk) * D]
+    ops.rotary_embedding_online(pos.to(gpu), gq, gk, D, 10000.0)
+    rtol = tol if dtype != torch.float32 else (3e-3, 1e-3)  # the fp32 angle's own rounding (pos_encoding.cu:84)
+    assert_close(gq.cpu().float(), ref_q.float(), *rtol, what + " q")
+    assert_close(gk.cpu().float(), ref_k.float(), *rtol, what + " k")
+    assert torch.equal(qkv_g[:, (hq + hk) * D:].cpu(), qkv[:, (hq + hk) * D:]), what + ": v part must be untouched"

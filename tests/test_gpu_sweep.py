@@ -3,7 +3,7 @@ tolerances of test_gpu_attention.py (bf16 2e-2 abs / 1e-2 rel, fp16 1e-2 / 5e-3;
 draws one configuration: head_dim, grouped query heads, causal / window / soft-cap, ragged and unequal Sq / Sk (so
 one-row calls go to the decode kernels and short query blocks to the split-KV kernels, as attention() routes them),
 dtype; rows of tie-heavy, NaN-holding or continuous scores, of 1 to 70,000 keys, for the selections; drawn widths
-and dtypes for the elementwise ops. The case is
+and dtypes for the elementwise ops; drawn shapes and sinks for the RoCo, SnapKV, Corm and KeyFormer cases. The case is
 printed before it runs. The column-score cases compare with the reference probabilities of
 test_gpu_attention.py (1e-3 rel)."""
 import numpy as np
@@ -199,3 +199,43 @@ def test_elementwise_random_shapes_match_oracle(gpu, seed):
     assert_close(gq.cpu().float(), ref_q.float(), *rtol, what + " q")
     assert_close(gk.cpu().float(), ref_k.float(), *rtol, what + " k")
     assert torch.equal(qkv_g[:, (hq + hk) * D:].cpu(), qkv[:, (hq + hk) * D:]), what + ": v part must be untouched"
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_selection_cases_random_shapes_match_oracle(gpu, seed):
+    # RoCo, SnapKV, Corm and KeyFormer (roco.py, snapkv.py, corm.py, kf.py) end to end on drawn shapes, with attention
+    # sinks, against the oracle (outputs fp16 1e-2 / 5e-3, scores 1e-3 rel; Corm's booleans up to exact ties)
+    from test_gpu_selection import _corm_check, _qkv
+
+    rng = np.random.default_rng(6000 + seed)
+    case = ["roco", "snapkv", "corm", "keyformer"][seed % 4]
+    S, H, D = int(rng.integers(2, 900)), int(rng.integers(1, 4)), int(rng.choice([64, 128]))
+    sinks = int(rng.integers(0, min(S, 8) + 1))
+    q, k, v = _qkv(S, H, D, 7000 + seed, sinks=sinks)
+    what = f"seed {seed}: {case} S{S} H{H} D{D} sinks{sinks}"
+    progress(what)
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    if case == "roco":
+        ref_out, ref_s1, ref_s2, _ = oa.roco(q, k, v)
+        out, s1, s2 = A.roco_attention(qg, kg, vg)
+        assert_close(s1.cpu(), ref_s1, 1e-6, 1e-3, what + " roco_score")
+        assert_close(s2.cpu(), ref_s2, 1e-6, 1e-3, what + " roco_sq_score")
+    elif case == "snapkv":
+        ks = int(rng.choice([1, 3, 5, 7]))
+        what += f" k{ks}"
+        ref_out, ref_score, _ = oa.snapkv(q, k, v, kernel_size=ks)
+        out, score = A.snapkv_attention(qg, kg, vg, kernel_size=ks)
+        assert_close(score.cpu(), ref_score, 1e-6, 1e-3, what + " snapkv_score")
+    elif case == "corm":
+        thr = oa.corm_mask(S, S)
+        ref_out, _, _ = oa.corm(q, k, v, thr)
+        out, hit = A.corm_attention(qg, kg, vg, thr.to(gpu))
+        _corm_check(hit, q, k, v, thr, what)
+    else:
+        tau = float(rng.choice([0.5, 1.0, 1.5, 3.0]))
+        what += f" tau{tau}"
+        er = oa.exp_rand(1, H, S, S, torch.Generator().manual_seed(seed))
+        ref_out, ref_score, _ = oa.keyformer(q, k, v, er, tau=tau)
+        out, score = A.keyformer_attention(qg, kg, vg, er.to(gpu), tau=tau)
+        assert_close(score.cpu(), ref_score, 1e-6, 1e-3, what + " kf_score")
+    assert_close(out.cpu().float(), ref_out.float(), 1e-2, 5e-3, what + " out")

@@ -1116,8 +1116,8 @@ extern "C" int dgg_roco_select_ws(const float* score, const float* sq_score, int
   const int R = (int)rows, N = (int)n;
   const int64_t chunks2 = (n + kSel2Chunk - 1) / kSel2Chunk;
   if (chunks2 * std::max(recent, budget) <= kSel2MaxCand && budget + recent <= kRocoMergeMax) {
-    // recent and pick in two stages (pick among other's mask), other in passes; the two index lists are written to
-    // out's rows (pick first) and merged in place
+    // recent and pick in two stages (pick among other's mask), other from recent's boundary; the two index lists
+    // are written to out's rows (pick first) and merged in place
     const int64_t rs = budget + recent;
     if (recent > 0)  // roco.py:56, leaving its boundary for `other`
       sel2_run(KeyStd{score, sq_score, N, rcp, 0}, R, N, (int)recent, ws, kSelAll, out_idx + budget, rs, st, true);

@@ -3,7 +3,8 @@ tolerances of test_gpu_attention.py (bf16 2e-2 abs / 1e-2 rel, fp16 1e-2 / 5e-3;
 draws one configuration: head_dim, grouped query heads, causal / window / soft-cap, ragged and unequal Sq / Sk (so
 one-row calls go to the decode kernels and short query blocks to the split-KV kernels, as attention() routes them),
 dtype; rows of tie-heavy, NaN-holding or continuous scores, of 1 to 70,000 keys, for the selections; drawn widths
-and dtypes for the elementwise ops; drawn shapes and sinks for the RoCo, SnapKV, Corm and KeyFormer cases. The case is
+and dtypes for the elementwise ops; drawn shapes and sinks for the RoCo, SnapKV, Corm and KeyFormer cases; drawn
+caches, split counts, indices and masks for decode, the KV-cache compaction, nonzero and the pooling. The case is
 printed before it runs. The column-score cases compare with the reference probabilities of
 test_gpu_attention.py (1e-3 rel)."""
 import numpy as np
@@ -239,3 +240,47 @@ def test_selection_cases_random_shapes_match_oracle(gpu, seed):
         out, score = A.keyformer_attention(qg, kg, vg, er.to(gpu), tau=tau)
         assert_close(score.cpu(), ref_score, 1e-6, 1e-3, what + " kf_score")
     assert_close(out.cpu().float(), ref_out.float(), 1e-2, 5e-3, what + " out")
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_decode_and_kv_ops_random_shapes_match_oracle(gpu, seed):
+    # decode_attention on the [B, Hkv, L, D] cache with a drawn split count (1 .. more splits than keys, at most
+    # 1,024), the KV-cache compaction with drawn indices, torch.nonzero's coordinates of a drawn mask, and SnapKV's
+    # pooling of drawn rows
+    rng = np.random.default_rng(8000 + seed)
+    B, Hkv = int(rng.integers(1, 4)), int(rng.integers(1, 5))
+    Hq, D = Hkv * int(rng.choice([1, 2, 4])), int(rng.choice([64, 128, 256]))
+    L = int(rng.integers(1, 3000))
+    splits = int(rng.choice([1, rng.integers(1, 65), min(1024, int(rng.integers(1, L + 8)))]))
+    dtype = torch.bfloat16 if rng.integers(0, 2) else torch.float16
+    what = f"seed {seed}: decode B{B} H{Hq}/{Hkv} L{L} D{D} splits{splits} {dtype}"
+    progress(what)
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hq, D, generator=g).to(dtype)
+    kc = torch.randn(B, Hkv, L, D, generator=g).to(dtype)
+    vc = torch.randn(B, Hkv, L, D, generator=g).to(dtype)
+    ref, ref_lse = oa.decode(q, kc, vc)
+    out, lse = A.decode_attention(q.to(gpu), kc.to(gpu), vc.to(gpu), splits=splits, return_lse=True)
+    assert_close(out.cpu().float(), ref.float(), *TOL[dtype], what)
+    assert_close(lse.cpu(), ref_lse, 2e-2, 1e-3, what + " lse")
+
+    S, n = int(rng.integers(1, 2000)), int(rng.integers(1, 600))
+    k = torch.randn(B, S, Hkv, D, generator=g).to(dtype)
+    v = torch.randn(B, S, Hkv, D, generator=g).to(dtype)
+    idx = torch.from_numpy(rng.integers(0, S, size=(B, Hkv, n))).long()
+    what = f"seed {seed}: kv_gather B{B} S{S} H{Hkv} D{D} n{n}"
+    progress(what)
+    got = A.kv_gather(k.to(gpu), v.to(gpu), idx.to(gpu)).cpu()
+    assert torch.equal(got, osel.kv_gather(k, v, idx)), what
+
+    shape = tuple(int(x) for x in rng.integers(1, 40, size=int(rng.integers(1, 4))))
+    mask = torch.from_numpy(rng.random(shape) < rng.random())
+    what = f"seed {seed}: nonzero {shape}"
+    progress(what)
+    assert torch.equal(A.nonzero(mask.to(gpu)).cpu(), osel.nonzero(mask)), what
+
+    x = torch.rand(int(rng.integers(1, 9)), int(rng.integers(1, 5000)), generator=g)
+    ks = int(rng.choice([1, 3, 5, 7, 9]))
+    what = f"seed {seed}: avg_pool1d {tuple(x.shape)} k{ks}"
+    progress(what)
+    assert_close(A.avg_pool1d(x.to(gpu), ks).cpu(), osel.avg_pool1d(x, ks), 1e-6, 1e-6, what)

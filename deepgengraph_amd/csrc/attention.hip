@@ -1123,21 +1123,29 @@ __device__ __forceinline__ void dma4(uint32_t lds, const void* vaddr) {
                : "memory", "m0");
 }
 
-template <typename T, int NW, int BQ, int NSTAGE, bool MASK, bool SOFTCAP, int REFROUND, bool LSE2, int EPI>
+// KPW: 32-key blocks per wave. With two, each Q fragment read from the LDS feeds two MFMAs (one per key block).
+template <typename T, int NW, int KPW, int BQ, int NSTAGE, bool MASK, bool SOFTCAP, int REFROUND, bool LSE2, int EPI>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_colsum_d128_kernel(AttnParams p) {
   constexpr int D = 128;
   constexpr int ROW_B = DmaLayout<D>::ROW_B, GROUP_B = DmaLayout<D>::GROUP_B;
   typedef typename T::scalar S;
   typedef typename T::vec8 V8;
-  constexpr int BK = 32 * NW;                // keys per workgroup
+  // With KPW key blocks per wave the waves form KPW row groups of NW / KPW waves: each group covers every key of
+  // the workgroup and takes its own BQ / KPW rows of each query tile; the groups' sums are added at the end.
+  constexpr int NG = KPW, NWG = NW / NG;     // row groups, waves per group
+  constexpr int BQW = BQ / NG;               // query rows of a tile per row group
+  constexpr int BK = 32 * KPW * NWG;         // keys per workgroup
   constexpr int QT_B = (BQ / 4) * GROUP_B;   // bytes of one Q tile
   constexpr int STAGE_B = QT_B + 4 * BQ;     // Q tile, then its BQ lse values
   constexpr int GPW = (BQ / 4) / NW;         // 4-row groups of a Q tile copied by each wave
   constexpr int NLSE = BQ / 64;              // lse copies per tile (last wave only)
-  constexpr int NMB = BQ / 32;
+  constexpr int NMB = BQW / 32;              // 32-row query blocks of a wave's part of a tile
   static_assert(GPW >= 1 && GPW * NW == BQ / 4, "Q tile groups must split over the waves");
-  static_assert(BQ % 64 == 0 && QT_B % 16 == 0, "tile shape");
+  static_assert(BQ % 64 == 0 && QT_B % 16 == 0 && BQW % 32 == 0 && NWG * NG == NW, "tile shape");
+  static_assert(KPW == 1 || ((EPI == kColSum || EPI == kColSumSq) && KPW == 2), "two key blocks: sum epilogues");
+  static_assert(NG == 1 || NSTAGE * STAGE_B >= 4 * 2 * BK, "the groups' sums are combined in the LDS");
+  constexpr int NSB = KPW * NMB;  // score blocks of a tile: block kp * NMB + mb (key block kp, query block mb)
   __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * STAGE_B];
 
   int kt, bh;
@@ -1146,24 +1154,30 @@ attn_colsum_d128_kernel(AttnParams p) {
   const int hk = h / p.group;
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 31, g = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wi = w % NWG, gw = w / NWG;  // wave within its row group, row group
+  const int rg0 = BQW * gw;              // first row of the group's part of a query tile
   const int k0 = kt * BK;
-  const int kw0 = k0 + 32 * w;  // first key of this wave
-  const int kj = kw0 + r;       // this lane's key
+  const int kw0 = k0 + 32 * KPW * wi;  // first key of this wave
+  const int kj = kw0 + r;             // this lane's key (of key block 0; block kp: kj + 32 kp)
 
   const S* kp = static_cast<const S*>(p.k) + b * p.k_sb + hk * p.k_sh;
   const char* qp = reinterpret_cast<const char*>(static_cast<const S*>(p.q) + b * p.q_sb + h * p.q_sh);
   const int64_t q_ss_b = p.q_ss * (int64_t)sizeof(S);
   const float* lsep = p.lse + (int64_t)bh * p.Sq;
 
-  V8 kf[D / 16];
+  V8 kf[KPW][D / 16];
 #pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk)  // back-to-back loads (keys past the end read the last key, zeroed below)
-    kf[kk] = ld16<V8>(kp + (int64_t)min(kj, p.Sk - 1) * p.k_ss + 16 * kk + 8 * g);
+  for (int kb = 0; kb < KPW; ++kb)
 #pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk) {
-    asm volatile("" : "+v"(kf[kk]));  // see the forward kernel
-    if (kj >= p.Sk) kf[kk] = V8{};
-  }
+    for (int kk = 0; kk < D / 16; ++kk)  // back-to-back loads (keys past the end read the last key, zeroed below)
+      kf[kb][kk] = ld16<V8>(kp + (int64_t)min(kj + 32 * kb, p.Sk - 1) * p.k_ss + 16 * kk + 8 * g);
+#pragma unroll
+  for (int kb = 0; kb < KPW; ++kb)
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+      asm volatile("" : "+v"(kf[kb][kk]));  // see the forward kernel
+      if (kj + 32 * kb >= p.Sk) kf[kb][kk] = V8{};
+    }
 
   // Query tiles that see any key of the workgroup, and of this wave.
   const int k_last = min(k0 + BK, p.Sk) - 1;
@@ -1174,25 +1188,29 @@ attn_colsum_d128_kernel(AttnParams p) {
   const int t_end = q_end > q_begin ? (q_end + BQ - 1) / BQ : t_begin;
   int wt_begin = t_begin, wt_end = t_begin;  // empty for a wave whose keys all lie past Sk
   if (kw0 < p.Sk) {
-    const int wk_last = min(kw0 + 32, p.Sk) - 1;
+    const int wk_last = min(kw0 + 32 * KPW, p.Sk) - 1;
     int wq_begin = 0, wq_end = p.Sq;
     if (p.causal) wq_begin = max(0, kw0 - p.offset);
     if (p.window > 0) wq_end = min(p.Sq, wk_last - p.offset + p.window);
-    if (wq_end > wq_begin) {
-      wt_begin = wq_begin / BQ;
-      wt_end = (wq_end + BQ - 1) / BQ;
+    if (wq_end > wq_begin) {  // tiles whose rows [t BQ + rg0, t BQ + rg0 + BQW) meet [wq_begin, wq_end)
+      const int y = wq_begin - rg0 - BQW + 1;
+      wt_begin = max(t_begin, y <= 0 ? 0 : (y + BQ - 1) / BQ);
+      const int z = wq_end - rg0;
+      wt_end = min(t_end, z <= 0 ? 0 : (z + BQ - 1) / BQ);
+      if (wt_end < wt_begin) wt_end = wt_begin;
     }
   }
-  // Tiles [t_full0, t_full1) need no mask for this wave: every row < Sq sees all 32 keys.
+  // Tiles [t_full0, t_full1) need no mask for this wave: every row < Sq sees all 32 KPW keys.
   int t_full0 = t_begin, t_full1 = t_end;
   if constexpr (MASK) {
     if (p.causal) {
-      const int a = kw0 + 31 - p.offset;  // first query row that sees the wave's last key
+      const int a = kw0 + 32 * KPW - 1 - p.offset - rg0;  // first row that sees the wave's last key, less rg0
       t_full0 = a <= 0 ? t_begin : min(t_end, max(t_begin, (a + BQ - 1) / BQ));
     }
     if (p.window > 0) {
       const int last = kw0 + p.window - p.offset - 1;  // last query row that sees the wave's first key
-      t_full1 = last < 0 ? t_full0 : min(t_end, (last + 1) / BQ);
+      const int v = last + 1 - rg0 - BQW + BQ;          // tiles t < v / BQ end their group rows by last
+      t_full1 = v <= 0 ? t_full0 : min(t_end, v / BQ);
     }
   }
   if (t_full1 * BQ > p.Sq) t_full1 = p.Sq / BQ;  // ragged last tile
@@ -1230,7 +1248,7 @@ attn_colsum_d128_kernel(AttnParams p) {
 
   // Q fragment (row 32mb + r, chunk 2kk + g) addressing, as the forward's K fragments.
   const int s4 = r & 3;
-  const uint32_t q_lane = (uint32_t)((r >> 2) * GROUP_B + s4 * ROW_B + 16 * g);
+  const uint32_t q_lane = (uint32_t)((rg0 / 4 + (r >> 2)) * GROUP_B + s4 * ROW_B + 16 * g);
   uint32_t xq[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) xq[i] = q_lane + 64u * (uint32_t)(i ^ s4);
@@ -1238,7 +1256,7 @@ attn_colsum_d128_kernel(AttnParams p) {
   constexpr bool PK = REFROUND && !SOFTCAP && std::is_same<T, F16>::value;
   const float c = PK ? kLog2e : score_coeff<SOFTCAP, REFROUND>(p);
   const float cy = EPI == kColKF ? c * p.kf_inv_tau : 0.f;  // KeyFormer: score -> exp2 domain / tau
-  ColAcc<EPI> acc;
+  ColAcc<EPI> acc[KPW];
   const int kjc = min(kj, p.Sk - 1);
   const float* erp = EPI == kColKF ? p.er + b * p.er_sb + h * p.er_sh : nullptr;  // KeyFormer exp_rand of (b, h)
   // KeyFormer exp_rand of (row, kjc) for tiles whose rows all exist: a wave-uniform tile address (scalar registers)
@@ -1248,7 +1266,7 @@ attn_colsum_d128_kernel(AttnParams p) {
   const uint32_t thr_lane_b = EPI == kColAnyGe ? (uint32_t)((4 * g * p.thr_rs + kjc) * 4) : 0u;
 
   // S = Q . K^T of query tile t (its LDS stage) into s.
-  auto qk_t = [&](const int t, f32x16 (&s)[NMB]) __attribute__((always_inline)) {
+  auto qk_t = [&](const int t, f32x16 (&s)[NSB]) __attribute__((always_inline)) {
     const uint32_t st = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B);
     uint32_t qb[4];  // opaque per-stage bases (reads at base + immediate offset)
 #pragma unroll
@@ -1257,38 +1275,42 @@ attn_colsum_d128_kernel(AttnParams p) {
       if constexpr (NSTAGE == 3) asm volatile("" : "+v"(qb[i]));
     }
 #pragma unroll
-    for (int mb = 0; mb < NMB; ++mb) s[mb] = f32x16{};
+    for (int i = 0; i < NSB; ++i) s[i] = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
 #pragma unroll
       for (int mb = 0; mb < NMB; ++mb) {
         const V8 a = lds_read<V8>(qb[kk >> 1] + mb * 8 * GROUP_B + 32 * (kk & 1));
-        s[mb] = mfma32(a, kf[kk], s[mb]);
+#pragma unroll
+        for (int kb = 0; kb < KPW; ++kb) s[kb * NMB + mb] = mfma32(a, kf[kb][kk], s[kb * NMB + mb]);
       }
     }
   };
-  auto epi_t = [&](const int t, const f32x16 (&sacc)[NMB], const float (&ev)[NMB][16], const float (&tv)[NMB][16],
+  auto epi_t = [&](const int t, const f32x16 (&sacc)[NSB], const float (&ev)[NMB][16], const float (&tv)[NMB][16],
                    auto masked) __attribute__((always_inline)) {
-    uint32_t lb = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B) + QT_B + 16 * g;  // this lane's lse values
+    uint32_t lb = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B) + QT_B + 4 * rg0 + 16 * g;  // this lane's lse
     if constexpr (NSTAGE == 3) asm volatile("" : "+v"(lb));
     // Visibility of (row o of the tile, this lane's key): causal rel >= 0, window rel < window, row < Sq.
-    const int rel0 = t * BQ + 4 * g + p.offset - kj;
-    const int rows_left = p.Sq - t * BQ - 4 * g;
+    const int rows_left = p.Sq - t * BQ - rg0 - 4 * g;
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb) {
       f32x4 lv[4];
 #pragma unroll
       for (int jq = 0; jq < 4; ++jq) lv[jq] = lds_read<f32x4>(lb + 4 * (32 * mb + 8 * jq));
+#pragma unroll
+      for (int kb = 0; kb < KPW; ++kb) {
+      const f32x16& sb = sacc[kb * NMB + mb];
+      const int rel0 = t * BQ + rg0 + 4 * g + p.offset - (kj + 32 * kb);
       f16x2 hs[8];
       if constexpr (PK) {
 #pragma unroll
-        for (int jp = 0; jp < 8; ++jp) hs[jp] = ref_scores_f16(sacc[mb][2 * jp], sacc[mb][2 * jp + 1], p);
+        for (int jp = 0; jp < 8; ++jp) hs[jp] = ref_scores_f16(sb[2 * jp], sb[2 * jp + 1], p);
       }
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         float x;
         if constexpr (PK) x = (float)hs[j >> 1][j & 1];
-        else x = score_value<T, SOFTCAP, REFROUND>(sacc[mb][j], p);
+        else x = score_value<T, SOFTCAP, REFROUND>(sb[j], p);
         const float l2 = LSE2 ? lv[j >> 2][j & 3] : lv[j >> 2][j & 3] * kLog2e;
         const int o = 32 * mb + 8 * (j >> 2) + (j & 3);
         float pe;
@@ -1308,8 +1330,9 @@ attn_colsum_d128_kernel(AttnParams p) {
           vis = ok;
         }
         // Corm compares visible pairs here; the masked ones (p = 0) are ORed in by corm_masked_or_kernel
-        if constexpr (EPI == kColAnyGe) acc.any |= vis && pe >= tv[mb][j];
-        else acc.add(pe, valid, min(t * BQ + 4 * g + o, p.Sq - 1), kjc, p);
+        if constexpr (EPI == kColAnyGe) acc[0].any |= vis && pe >= tv[mb][j];
+        else acc[kb].add(pe, valid, min(t * BQ + rg0 + 4 * g + o, p.Sq - 1), min(kjc + 32 * kb, p.Sk - 1), p);
+      }
       }
     }
   };
@@ -1359,7 +1382,7 @@ attn_colsum_d128_kernel(AttnParams p) {
             tv[mb][j] = p.thr[(int64_t)min(t * BQ + 4 * g + 32 * mb + 8 * (j >> 2) + (j & 3), p.Sq - 1) * p.thr_rs + kjc];
       }
     }
-    f32x16 sacc[NMB];
+    f32x16 sacc[NSB];
     qk_t(t, sacc);
     epi_t(t, sacc, ev, tv, masked);
   };
@@ -1370,58 +1393,69 @@ attn_colsum_d128_kernel(AttnParams p) {
   // Corm: whether this wave's keys are all decided (no tile of its range left, or every key flagged).
   bool wave_done = wt_begin >= wt_end;
   // One pipelined step: the mask-free epilogue of tile t (scores in sc) and S of tile t+1 (into sn), in a fixed
-  // order of 32 fenced steps, one per MFMA: the Q fragment read two steps ahead, the QK^T MFMA (k-step i/4, block
-  // i%4), the exponentials and sums of score pair i%8 of block i/8, and every second step the lse values of the
-  // pairs two steps ahead. (Left to the compiler, the 32 fragment reads move to the front and the form spills.)
-  auto pipe_step = [&](const int t, const f32x16 (&sc)[NMB], f32x16 (&sn)[NMB]) __attribute__((always_inline)) {
-    static_assert(NMB == 4, "32 steps: 8 k-steps x 4 blocks, 4 blocks x 8 score pairs");
+  // order of 32 fenced steps, one per MFMA. Step i runs the QK^T MFMA of Q fragment f = i / KPW (k-step f / NMB,
+  // query block f % NMB) with key block i % KPW, reads fragment f + 2 when it starts a fragment, and takes the
+  // exponentials and sums of score pair q = i / KPW (pair q % 8 of query block q / 8) of that key block; the lse
+  // values of the next four rows are read when a group of two pairs starts. (Left to the compiler, the fragment
+  // reads move to the front and the form spills.)
+  auto pipe_step = [&](const int t, const f32x16 (&sc)[NSB], f32x16 (&sn)[NSB]) __attribute__((always_inline)) {
+    static_assert(NSB == 4, "32 steps: 8 k-steps x 4 score blocks, 4 score blocks x 8 score pairs");
+    constexpr int NF = 32 / KPW;       // Q fragments of a tile
+    constexpr int NLG = 16 / KPW;      // groups of two score pairs (four rows' lse values) per key block
     const uint32_t stc = smem_base + (uint32_t)((t % NSTAGE) * STAGE_B);
     const uint32_t stn = smem_base + (uint32_t)(((t + 1) % NSTAGE) * STAGE_B);
     // per-stage base registers, opaque to the compiler, so that every read is base + immediate offset
-    uint32_t qb[4], lb = stc + QT_B + 16 * g;
+    uint32_t qb[4], lb = stc + QT_B + 4 * rg0 + 16 * g;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       qb[i] = stn + xq[i];
       asm volatile("" : "+v"(qb[i]));
     }
     asm volatile("" : "+v"(lb));
-    auto qread = [&](const int i) __attribute__((always_inline)) {
-      const int kk = i >> 2, mb = i & 3;
+    auto qread = [&](const int f) __attribute__((always_inline)) {
+      const int kk = f / NMB, mb = f % NMB;
       return lds_read<V8>(qb[kk >> 1] + mb * 8 * GROUP_B + 32 * (kk & 1));
     };
-    auto lread = [&](const int i) __attribute__((always_inline)) {  // lse of the rows of pairs i, i+1 (i even)
-      return lds_read<f32x4>(lb + 4 * (32 * (i >> 3) + 8 * ((i & 7) >> 1)));
+    auto lread = [&](const int lg) __attribute__((always_inline)) {  // lse of the rows of pairs 2lg, 2lg+1
+      return lds_read<f32x4>(lb + 4 * (32 * (lg >> 2) + 8 * (lg & 3)));
     };
 #pragma unroll
-    for (int mb = 0; mb < NMB; ++mb) sn[mb] = f32x16{};
-    V8 a[3];
+    for (int i = 0; i < NSB; ++i) sn[i] = f32x16{};
+    // Q fragment ring: fragment f + NA - 1 is read when fragment f starts (two steps ahead with one key block,
+    // two fragments, i.e. four steps, with two; with two key blocks a two-slot ring still reads two steps ahead)
+    constexpr int NA = KPW == 2 ? 2 : 3;
+    V8 a[NA];
     f32x4 lvb[2];
-    a[0] = qread(0);
-    a[1] = qread(1);
+#pragma unroll
+    for (int j = 0; j < NA - 1; ++j) a[j] = qread(j);
     lvb[0] = lread(0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-      if (i + 2 < 32) a[(i + 2) % 3] = qread(i + 2);
-      if ((i & 1) == 0 && i + 2 < 32) lvb[((i + 2) >> 1) & 1] = lread(i + 2);
-      sn[i & 3] = mfma32(a[i % 3], kf[i >> 2], sn[i & 3]);
-      const int mb = i >> 3, jp = i & 7;
-      const f32x4& lv = lvb[(i >> 1) & 1];
+      const int f = i / KPW, kb = i % KPW;
+      if (kb == 0 && f + NA - 1 < NF) a[(f + NA - 1) % NA] = qread(f + NA - 1);
+      const int q = i / KPW, lg = q >> 1;
+      if (i % (2 * KPW) == 0 && lg + 1 < NLG) lvb[(lg + 1) & 1] = lread(lg + 1);
+      sn[kb * NMB + f % NMB] = mfma32(a[f % NA], kf[kb][f / NMB], sn[kb * NMB + f % NMB]);
+      const int mb = q >> 3, jp = q & 7;
+      const f32x16& sp = sc[kb * NMB + mb];
+      const f32x4& lv = lvb[lg & 1];
       float x[2];
       if constexpr (PK) {
-        const f16x2 hs = ref_scores_f16(sc[mb][2 * jp], sc[mb][2 * jp + 1], p);
+        const f16x2 hs = ref_scores_f16(sp[2 * jp], sp[2 * jp + 1], p);
         x[0] = (float)hs[0];
         x[1] = (float)hs[1];
       } else {
-        x[0] = score_value<T, SOFTCAP, REFROUND>(sc[mb][2 * jp], p);
-        x[1] = score_value<T, SOFTCAP, REFROUND>(sc[mb][2 * jp + 1], p);
+        x[0] = score_value<T, SOFTCAP, REFROUND>(sp[2 * jp], p);
+        x[1] = score_value<T, SOFTCAP, REFROUND>(sp[2 * jp + 1], p);
       }
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const float l2 = LSE2 ? lv[2 * (jp & 1) + e] : lv[2 * (jp & 1) + e] * kLog2e;
-        acc.add(fast_exp2(fmaf(x[e], c, -l2)), true, 0, kjc, p);
+        acc[kb].add(fast_exp2(fmaf(x[e], c, -l2)), true, 0, kjc, p);
       }
-      acc.pin();
+#pragma unroll
+      for (int k2 = 0; k2 < KPW; ++k2) acc[k2].pin();
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -1464,7 +1498,7 @@ attn_colsum_d128_kernel(AttnParams p) {
       tile(t, masked);
       if constexpr (EPI == kColAnyGe) {
         // this lane's key is decided when either half of its rows flagged it (keys past the end count as decided)
-        const bool decided = (acc.any | __shfl_xor(acc.any, 32, 64)) != 0 || kj >= p.Sk;
+        const bool decided = (acc[0].any | __shfl_xor(acc[0].any, 32, 64)) != 0 || kj >= p.Sk;
         wave_done = t + 1 >= wt_end || __all(decided);
       }
     }
@@ -1475,7 +1509,7 @@ attn_colsum_d128_kernel(AttnParams p) {
   // The mask-free range lies inside the wave's range whenever the wave has keys (kw0 < Sk).
   if (PIPE && t_full1 - t_full0 >= 2 && t_full0 >= wt_begin && t_full1 <= wt_end) {
     // scores of two tiles in flight, in two buffers that swap roles every step (loop unrolled by two)
-    f32x16 sa[NMB], sb[NMB];
+    f32x16 sa[NSB], sb[NSB];
     float none[NMB][16];  // KeyFormer / Corm inputs, never read by these epilogues
     int t = t_full0;
     sync(t);
@@ -1501,7 +1535,35 @@ attn_colsum_d128_kernel(AttnParams p) {
   }
   for (int t = t_full1; go && t < t_end; ++t) go = step(t, std::true_type{});
 
-  acc.store(p, bh, kj, g);
+  if constexpr (NG == 1) {
+    acc[0].store(p, bh, kj, g);
+  } else {
+    // Row group 1 leaves its sums (lane halves added) in the LDS; group 0 adds them to its own and stores.
+    wait_vmem<0>();
+    __syncthreads();  // every wave is done with the Q stages
+    float* red = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (int kb = 0; kb < KPW; ++kb) {
+      acc[kb].s += __shfl_xor(acc[kb].s, 32, 64);
+      if constexpr (EPI == kColSumSq) acc[kb].s2 += __shfl_xor(acc[kb].s2, 32, 64);
+      const int key = 32 * (KPW * wi + kb) + r;  // key within the workgroup
+      if (gw == 1 && g == 0) {
+        red[key] = acc[kb].s;
+        if constexpr (EPI == kColSumSq) red[BK + key] = acc[kb].s2;
+      }
+    }
+    __syncthreads();
+    if (gw == 0 && g == 0) {
+#pragma unroll
+      for (int kb = 0; kb < KPW; ++kb) {
+        const int key = 32 * (KPW * wi + kb) + r, kjb = kj + 32 * kb;
+        if (kjb < p.Sk) {
+          p.colsum[(int64_t)bh * p.Sk + kjb] = acc[kb].s + red[key];
+          if constexpr (EPI == kColSumSq) p.colsum2[(int64_t)bh * p.Sk + kjb] = acc[kb].s2 + red[BK + key];
+        }
+      }
+    }
+  }
 }
 
 template <typename T, int D, int BN, bool MASK, bool SOFTCAP, int REFROUND>
@@ -1604,6 +1666,10 @@ void pick_fwd(const AttnParams& p, bool ref, hipStream_t st) {
 #ifndef DGG_COL_PIPE
 #define DGG_COL_PIPE 1
 #endif
+// DGG_COL_KPW: 32-key blocks per wave in the pipelined form (2; 1: 8 waves x 32 keys over 128-row tiles).
+#ifndef DGG_COL_KPW
+#define DGG_COL_KPW 2
+#endif
 constexpr int kC128NW = 8, kC128BQ = 128, kC128NS = 2;
 constexpr int kC128BK = 32 * kC128NW;  // keys per workgroup (head_dim 128)
 
@@ -1611,13 +1677,19 @@ template <typename T, bool MASK, bool SOFTCAP, int REFROUND, int EPI>
 void launch_colsum_d128(const AttnParams& p, hipStream_t st) {
   const unsigned grid = (unsigned)p.n_tiles * p.B * p.Hq;
   // (the reference-rounded soft-cap's score chain is too long for a fixed-order step: it keeps the plain form)
-  constexpr int NS = DGG_COL_PIPE && (EPI == kColSum || EPI == kColSumSq) && !(SOFTCAP && REFROUND) ? 3 : kC128NS;
+  constexpr bool PIPE = DGG_COL_PIPE && (EPI == kColSum || EPI == kColSumSq) && !(SOFTCAP && REFROUND);
+  constexpr int NS = PIPE ? 3 : kC128NS;
+  // The pipelined form: 64 keys per wave, the 8 waves in two row groups of 4 (each group takes 64 rows of every
+  // 128-row query tile); the same 256 keys per workgroup.
+  constexpr int KPW = PIPE ? DGG_COL_KPW : 1;
+  constexpr int NW = kC128NW, BQ = kC128BQ;
+  static_assert(32 * NW == kC128BK, "keys per workgroup");
   if (p.lse_base2)
-    hipLaunchKernelGGL((attn_colsum_d128_kernel<T, kC128NW, kC128BQ, NS, MASK, SOFTCAP, REFROUND, true, EPI>),
-                       dim3(grid), dim3(64 * kC128NW), 0, st, p);
+    hipLaunchKernelGGL((attn_colsum_d128_kernel<T, NW, KPW, BQ, NS, MASK, SOFTCAP, REFROUND, true, EPI>),
+                       dim3(grid), dim3(64 * NW), 0, st, p);
   else
-    hipLaunchKernelGGL((attn_colsum_d128_kernel<T, kC128NW, kC128BQ, NS, MASK, SOFTCAP, REFROUND, false, EPI>),
-                       dim3(grid), dim3(64 * kC128NW), 0, st, p);
+    hipLaunchKernelGGL((attn_colsum_d128_kernel<T, NW, KPW, BQ, NS, MASK, SOFTCAP, REFROUND, false, EPI>),
+                       dim3(grid), dim3(64 * NW), 0, st, p);
 }
 
 template <typename T, int D, bool MASK, bool SOFTCAP, int REFROUND, int EPI>

@@ -373,6 +373,11 @@ def test_colsum_variants(gpu, D, Sq, Sk, causal, window, softcap, dtype, base2):
     (256, 256, 4, 2, False, 0, torch.float16),     # exactly two mask-free query tiles: the shortest pipelined run
     (900, 1100, 4, 4, True, 500, torch.float16),   # window, Sq < Sk, ragged ends
     (1030, 1030, 4, 2, True, 0, torch.bfloat16),   # GQA, ragged last query tile
+    # 64 keys per wave in two row groups: the second group's rows of the last query tile all past Sq, a wave's
+    # second key block partly past Sk; a window shorter than a wave's keys; no mask with Sq < Sk and GQA
+    (1088, 1000, 4, 2, True, 0, torch.float16),
+    (1200, 1200, 2, 2, True, 40, torch.bfloat16),
+    (700, 1500, 2, 1, False, 0, torch.float16),
 ])
 def test_colscore_sum_and_sumsq_variants(gpu, Sq, Sk, Hq, Hkv, causal, window, dtype):
     # RoCo's epilogue (sums of p and p^2, roco.py:43-47) through the column-score primitive on the shapes the

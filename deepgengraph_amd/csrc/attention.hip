@@ -1200,7 +1200,7 @@ attn_colsum_d128_kernel(AttnParams p) {
       if (wt_end < wt_begin) wt_end = wt_begin;
     }
   }
-  // Tiles [t_full0, t_full1) need no mask for this wave: every row < Sq sees all 32 KPW keys.
+  // Tiles [t_full0, t_full1) need no mask for this wave: every row < Sq of its part sees all of its 32 * KPW keys.
   int t_full0 = t_begin, t_full1 = t_end;
   if constexpr (MASK) {
     if (p.causal) {
@@ -1394,7 +1394,7 @@ attn_colsum_d128_kernel(AttnParams p) {
   bool wave_done = wt_begin >= wt_end;
   // One pipelined step: the mask-free epilogue of tile t (scores in sc) and S of tile t+1 (into sn), in a fixed
   // order of 32 fenced steps, one per MFMA. Step i runs the QK^T MFMA of Q fragment f = i / KPW (k-step f / NMB,
-  // query block f % NMB) with key block i % KPW, reads fragment f + 2 when it starts a fragment, and takes the
+  // query block f % NMB) with key block i % KPW, reads a later fragment when it starts a fragment, and takes the
   // exponentials and sums of score pair q = i / KPW (pair q % 8 of query block q / 8) of that key block; the lse
   // values of the next four rows are read when a group of two pairs starts. (Left to the compiler, the fragment
   // reads move to the front and the form spills.)
@@ -1421,8 +1421,9 @@ attn_colsum_d128_kernel(AttnParams p) {
     };
 #pragma unroll
     for (int i = 0; i < NSB; ++i) sn[i] = f32x16{};
-    // Q fragment ring: fragment f + NA - 1 is read when fragment f starts (two steps ahead with one key block,
-    // two fragments, i.e. four steps, with two; with two key blocks a two-slot ring still reads two steps ahead)
+    // Q fragment ring of NA slots: fragment f + NA - 1 is read when fragment f starts, two steps before its first
+    // MFMA either way (one key block: three slots, two fragments ahead; two key blocks: two slots, one fragment
+    // ahead, each fragment feeding two steps)
     constexpr int NA = KPW == 2 ? 2 : 3;
     V8 a[NA];
     f32x4 lvb[2];

@@ -143,6 +143,57 @@ def test_colscore_random_launches_match_reference(gpu, seed):
         _colsum_check(cs, _colsum_reference(q, k, causal, softcap, window).float(), what + " sum")
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_colscore_long_random_launches_match_reference(gpu, seed):
+    # the head_dim-128 column pass on drawn shapes long enough for long software-pipelined runs of its 64-key waves
+    # (several 128-row query tiles per wave, ragged ends, windows, GQA), H2O sums or RoCo's sums and sums of squares,
+    # against the reference's probabilities at the column-sum contract (1e-3 rel)
+    from deepgengraph_amd import _lib
+    from test_gpu_attention import _colsum_check, _colsum_reference
+
+    rng = np.random.default_rng(4500 + seed)
+    D = 128
+    Hkv = int(rng.choice([1, 2]))
+    Hq = Hkv * int(rng.choice([1, 2]))
+    Sq, Sk = int(rng.integers(700, 2400)), int(rng.integers(700, 2400))
+    causal = bool(rng.integers(0, 4))
+    sumsq = bool(rng.integers(0, 2))
+    softcap = 30.0 if not sumsq and rng.integers(0, 4) == 0 else 0.0
+    window = int(rng.integers(1, Sk + 1)) if causal and rng.integers(0, 3) == 0 else 0
+    dtype = torch.bfloat16 if rng.integers(0, 2) else torch.float16
+    base2 = bool(rng.integers(0, 2))
+    what = (f"seed {seed}: Sq{Sq} Sk{Sk} H{Hq}/{Hkv} D{D} {dtype} causal={causal} cap={softcap} win={window} "
+            f"base2={base2} sumsq={sumsq}")
+    progress(what)
+    g = torch.Generator().manual_seed(100 + seed)
+    q = torch.randn(1, Sq, Hq, D, generator=g).to(dtype)
+    k = torch.randn(1, Sk, Hkv, D, generator=g).to(dtype)
+    v = torch.randn(1, Sk, Hkv, D, generator=g).to(dtype)
+    kw = dict(causal=causal, window=window, lse_base2=base2)
+    _, lse = A.attention(q.to(gpu), k.to(gpu), v.to(gpu), return_lse=True, ref_rounding=True, softcap=softcap, **kw)
+    # bf16 scores: two fp32 accumulation orders of the same dot product (the MFMA's, the CPU matmul's, which itself
+    # varies with the host's instruction set) can round to neighbouring bf16 values, which moves that probability
+    # by up to |s| * 2^-8; in a short windowed column one such score can shift a sum of squares by ~1e-3. The exact
+    # invariant below (each row that sees a key contributes 1 to the sums) holds either way.
+    def check(got, ref, label):
+        if dtype == torch.bfloat16:
+            assert_close(got, ref, 1e-6, 4e-3, what + label)
+        else:
+            _colsum_check(got, ref, what + label)
+    if sumsq:
+        s1, s2 = A.attention_colscore(q.to(gpu), k.to(gpu), lse, epilogue=_lib.COL_SUM_SQ, ref_rounding=True, **kw)
+        ref1 = _colsum_reference(q, k, causal, 0.0, window)
+        check(s1.cpu(), ref1.float(), " sum")
+        check(s2.cpu(), _colsum_reference(q, k, causal, 0.0, window, power=2).float(), " sum of squares")
+        got1, rows = s1.cpu(), ref1.sum(-1)
+    else:
+        ref1 = _colsum_reference(q, k, causal, softcap, window)
+        got1 = A.attention_colsum(q.to(gpu), k.to(gpu), lse, softcap=softcap, **kw).cpu()
+        check(got1, ref1.float(), " sum")
+        rows = ref1.sum(-1)
+    assert_close(got1.double().sum(-1), torch.round(rows), 0, 1e-5, what + " sum over keys = rows that see a key")
+
+
 def _draw_width(rng):
     """A row width: a multiple of 8 (the vector paths) or not (the scalar ones), small or wide."""
     w = int(rng.integers(1, 8193))
